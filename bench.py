@@ -1,0 +1,267 @@
+"""MLA decode benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload dense|skew|sparse|sparse_fp8]
+
+A step is one decode of the whole batch through the public path: scheduler metadata
+(get_mla_metadata) + decode + split combine, with every input already resident in HBM.
+The default workload is BASELINE config 2 (dense bf16, B=64, h_q=128, s_q=1, lengths
+U[4096, 8192], 64-token pages through a permuted block table).  KV pools are rotated
+between steps so consecutive steps do not hit the 256 MB last-level cache.
+
+Prints one JSON line: value = wall-clock us/step (lower is better); `roofline` is the
+decode kernel alone (HIP events around its launch on the launch stream), algorithmic
+bytes / FLOPs per launch over its mean duration; `cpu_baseline` is the CPU oracle
+(the reference's PyTorch math restated) timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "MLA decode µs/step + achieved HBM GB/s & MFMA TFLOPS (% of roofline), B=64 h=128"
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+SCALE = 192 ** -0.5
+PAGE = 64
+
+
+def workload_spec(name: str) -> dict:
+    if name == "dense":
+        return dict(name="dense_bf16_cfg2", batch=64, h_q=128, s_q=1, causal=False,
+                    lens=("uniform", 4096, 8192), topk=None, fp8=False, seed=2)
+    if name == "skew":
+        return dict(name="dense_bf16_skew_cfg3", batch=32, h_q=128, s_q=2, causal=True,
+                    lens=("lognormal", 4096, 1.0, 128, 65536), topk=None, fp8=False, seed=3)
+    if name == "sparse":
+        return dict(name="sparse_bf16_top2048_cfg4", batch=64, h_q=128, s_q=1, causal=False,
+                    lens=("const", 32768), topk=2048, fp8=False, seed=4)
+    if name == "sparse_fp8":
+        return dict(name="sparse_fp8_top2048_cfg5", batch=128, h_q=128, s_q=1, causal=False,
+                    lens=("const", 65536), topk=2048, fp8=True, seed=5)
+    raise SystemExit(f"unknown workload {name}")
+
+
+def make_lens(spec, gen) -> torch.Tensor:
+    kind = spec["lens"][0]
+    b = spec["batch"]
+    if kind == "uniform":
+        return torch.randint(spec["lens"][1], spec["lens"][2] + 1, (b,), generator=gen,
+                             dtype=torch.int32)
+    if kind == "lognormal":
+        _, med, sigma, lo, hi = spec["lens"]
+        x = torch.exp(math.log(med) + sigma * torch.randn((b,), generator=gen))
+        return x.round().clamp(lo, hi).to(torch.int32)
+    return torch.full((b,), spec["lens"][1], dtype=torch.int32)
+
+
+def build_inputs(spec, dev, copies):
+    """Synthetic inputs on the GPU: q, `copies` KV pools (+ their block tables), lens,
+    indices.  Values N(0,1)*0.1 in bf16 (fp8: quantised per 128-dim tile)."""
+    gen = torch.Generator().manual_seed(spec["seed"])
+    lens = make_lens(spec, gen)
+    nblk = [-(-int(x) // PAGE) for x in lens]
+    pool = sum(nblk)
+    maxb = max(nblk)
+    dgen = torch.Generator(device=dev).manual_seed(spec["seed"])
+    q = (torch.randn((spec["batch"], spec["s_q"], spec["h_q"], 576), generator=dgen,
+                     device=dev) * 0.1).to(torch.bfloat16)
+    pools, tables = [], []
+    for _ in range(copies):
+        perm = torch.randperm(pool, generator=gen).to(torch.int32)
+        bt = torch.zeros((spec["batch"], maxb), dtype=torch.int32)
+        off = 0
+        for b, n in enumerate(nblk):
+            bt[b, :n] = perm[off:off + n]
+            off += n
+        tables.append(bt.to(dev))
+        if spec["fp8"]:
+            kc = torch.empty((pool, PAGE, 1, 656), dtype=torch.uint8, device=dev)
+            chunk = 1024
+            for c0 in range(0, pool, chunk):
+                c1 = min(pool, c0 + chunk)
+                lat = torch.randn((c1 - c0, PAGE, 1, 512), generator=dgen, device=dev) * 0.1
+                u = torch.rand((c1 - c0, PAGE, 1, 4), generator=dgen, device=dev)
+                sc = torch.exp(math.log(1e-3) + u * (math.log(1e-1) - math.log(1e-3)))
+                codes = (lat.view(c1 - c0, PAGE, 1, 4, 128) / sc.unsqueeze(-1)).clamp(-448, 448)
+                codes = codes.to(torch.float8_e4m3fn).view(torch.uint8).view(c1 - c0, PAGE, 1, 512)
+                rope = (torch.randn((c1 - c0, PAGE, 1, 64), generator=dgen, device=dev)
+                        * 0.1).to(torch.bfloat16)
+                kc[c0:c1] = torch.cat([codes, sc.contiguous().view(torch.uint8),
+                                       rope.view(torch.uint8)], dim=-1)
+        else:
+            kc = (torch.randn((pool, PAGE, 1, 576), generator=dgen, device=dev) * 0.1).to(
+                torch.bfloat16)
+        pools.append(kc)
+    indices = None
+    if spec["topk"]:
+        topk = spec["topk"]
+        b, s_q = spec["batch"], spec["s_q"]
+        n = int(lens[0])
+        r = torch.rand((b * s_q, n), generator=dgen, device=dev)
+        indices = torch.topk(r, topk, dim=1).indices.to(torch.int32).view(b, s_q, topk)
+        drop = torch.rand((b, s_q, topk), generator=dgen, device=dev) < 0.02
+        indices = torch.where(drop, torch.full_like(indices, -1), indices).contiguous()
+    return q, pools, tables, lens.to(dev), indices
+
+
+def algorithmic_work(spec, lens_cpu, indices) -> tuple:
+    """HBM bytes and FLOPs one decode launch must move / compute."""
+    b, s_q, h_q = spec["batch"], spec["s_q"], spec["h_q"]
+    row_bytes = 656 if spec["fp8"] else 1152
+    if spec["topk"]:
+        n_valid = int((indices >= 0).sum())  # per (b, s) token lists
+        kv_rows = n_valid
+        table = indices.numel() * 4
+        flops_rows = n_valid  # each valid (b, s, token) pair meets h_q heads once
+    else:
+        kv_rows = int(lens_cpu.sum())
+        table = sum(-(-int(x) // PAGE) for x in lens_cpu) * 4
+        flops_rows = kv_rows * s_q
+    nbytes = kv_rows * row_bytes + b * s_q * h_q * (576 * 2 + 512 * 2 + 4) + table
+    flops = flops_rows * h_q * 2 * (576 + 512)
+    return nbytes, flops
+
+
+def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
+    """The oracle (fp32 PyTorch restatement of the reference's CPU path) on a bounded
+    sample of the workload's sequences, scaled to a full step."""
+    from oracle import mla_oracle as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    b = spec["batch"]
+    sample = 1
+    lens_c = lens.cpu()
+    sel = list(range(b))
+
+    def run(nseq):
+        idx = sel[:nseq]
+        need = torch.unique(table[idx].flatten()).long()
+        # copy only the pages these sequences use, then remap the table
+        remap = torch.full((pool.shape[0],), -1, dtype=torch.long, device=pool.device)
+        remap[need] = torch.arange(need.numel(), device=pool.device)
+        kc = pool[need].cpu()
+        bt = remap[table[idx].long()].to(torch.int32).cpu()
+        qc = q[idx].cpu()
+        t0 = time.perf_counter()
+        if spec["topk"]:
+            orc.sparse_decode_ref(qc, kc, bt, lens_c[idx], indices[idx].cpu(), SCALE,
+                                  is_fp8=spec["fp8"])
+        else:
+            orc.dense_decode_ref(qc, kc, bt, lens_c[idx], SCALE, spec["causal"])
+        return time.perf_counter() - t0
+
+    t1 = run(1)
+    sample = max(1, min(b, int(15.0 / max(t1, 1e-3))))
+    times = [run(sample) for _ in range(3)]
+    t = sorted(times)[1]
+    us_step = t / sample * b * 1e6
+    return {"value": round(us_step, 1), "unit": "µs/step", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{sample} of {b} sequences of {spec['name']}, median of 3, "
+                      f"scaled x{b / sample:.2f} to the full step"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="dense",
+                    choices=["dense", "skew", "sparse", "sparse_fp8"])
+    ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(batch sharding across GPUs needs no exchange: run one process per GPU).",
+              file=sys.stderr)
+        raise SystemExit(2)
+
+    import flagattention_amd as fa
+
+    dev = torch.device("cuda:0")
+    spec = workload_spec(args.workload)
+    q, pools, tables, lens, indices = build_inputs(spec, dev, args.copies)
+    s_q, h_q, b = spec["s_q"], spec["h_q"], spec["batch"]
+    md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, topk=spec["topk"])
+    ws = fa.DecodeWorkspace(b, s_q, h_q, md.shape[0], dev, topk=spec["topk"])
+
+    def step(i, events=None):
+        md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, topk=spec["topk"])
+        c = i % len(pools)
+        return ws.run(q, pools[c], tables[c], lens, md, ns, SCALE, spec["causal"],
+                      spec["fp8"], indices, decode_events=events)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    us_step = (t1 - t0) / args.steps * 1e6
+    dec_ms = sorted(s.elapsed_time(e) for s, e in evs)
+    dec_us_mean = sum(dec_ms) / len(dec_ms) * 1e3
+    dec_us_med = dec_ms[len(dec_ms) // 2] * 1e3
+
+    lens_cpu = lens.cpu()
+    nbytes, flops = algorithmic_work(spec, lens_cpu, indices.cpu() if indices is not None else None)
+    gbs = nbytes / (dec_us_mean * 1e-6) / 1e9
+    tflops = flops / (dec_us_mean * 1e-6) / 1e12
+    hbm_frac = gbs / PEAK_HBM_GBS
+    mfma_frac = tflops / PEAK_BF16_TFLOPS
+    # the bound is the roof with the larger required time at peak
+    bound = "hbm" if nbytes / PEAK_HBM_GBS >= flops / (PEAK_BF16_TFLOPS * 1e3) else "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(hbm_frac, 4), "traffic": None}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(mfma_frac, 4), "traffic": None}
+    roof.update({"kernel": "mla_decode_kernel", "kernel_us_mean": round(dec_us_mean, 2),
+                 "kernel_us_median": round(dec_us_med, 2), "bytes_per_launch": nbytes,
+                 "flops_per_launch": flops, "hbm_gbs": round(gbs, 1),
+                 "hbm_frac": round(hbm_frac, 4), "mfma_tflops": round(tflops, 1),
+                 "mfma_frac": round(mfma_frac, 4)})
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(spec, q, pools[0], tables[0], lens, indices)
+
+    rec = {
+        "metric": METRIC,
+        "value": round(us_step, 2),
+        "unit": "µs/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if not spec["fp8"] else "fp8-e4m3 KV, bf16 MFMA",
+        "data": "synthetic",
+        "config": {"workload": spec["name"], "batch": b, "h_q": h_q, "s_q": s_q,
+                   "d_qk": 576, "d_v": 512, "page": PAGE, "causal": spec["causal"],
+                   "topk": spec["topk"], "mean_seqlen": float(lens_cpu.float().mean()),
+                   "num_parts": int(md.shape[0]), "kv_pool_copies": len(pools)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,87 @@
+// LSE-weighted split combine.
+//
+// Math follows the reference's LSE form (src/flag_attn/split_kv.py:198-228):
+//   lse = logsumexp_s(lse_s),  out = sum_s exp(lse_s - lse) * o_s
+// where o_s is the split's already-normalised output and lse_s its natural-log
+// normaliser.  Empty splits carry lse_s = -inf and weigh nothing; a sequence
+// whose every split is empty (or that has no split at all) gets out = 0 and
+// lse = -inf, the convention of src/flag_attn/split_kv.py:161-164.
+//
+// One 64-lane wave per (sequence, query row); each lane owns 8 of the 512
+// value dims, so the fp32 partial rows are read as two 16-byte loads per lane.
+#include "fa_common.h"
+
+namespace fa {
+namespace {
+
+constexpr int kCombineThreads = 256;
+constexpr int kRowsPerBlock = kCombineThreads / 64;
+
+__global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
+    const float* __restrict__ o_accum, const float* __restrict__ lse_accum,
+    const int32_t* __restrict__ num_splits, bf16* __restrict__ out, float* __restrict__ lse,
+    int s_q, int h_q, int max_split) {
+  const int rows = s_q * h_q;
+  const int b = blockIdx.y;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int s0 = num_splits[b];
+  const int ns = num_splits[b + 1] - s0;
+  if (ns == 1) return;  // written directly by the decode kernel
+  if (s0 < 0 || ns < 0 || s0 + ns > max_split) return;  // inconsistent metadata
+
+  const int s = row / h_q, h = row - s * h_q;
+  bf16* orow = out + ((static_cast<long long>(b) * s_q + s) * h_q + h) * kDv + lane * 8;
+  float* lse_out = lse + (static_cast<long long>(b) * h_q + h) * s_q + s;
+  const float ninf = -__builtin_inff();
+
+  float mx = ninf;
+  for (int i = 0; i < ns; ++i)
+    mx = fmaxf(mx, lse_accum[static_cast<long long>(s0 + i) * rows + row]);
+
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  float total = ninf;
+  if (mx != ninf) {
+    float sum = 0.f;
+    for (int i = 0; i < ns; ++i)
+      sum += expf(lse_accum[static_cast<long long>(s0 + i) * rows + row] - mx);
+    total = mx + logf(sum);
+    for (int i = 0; i < ns; ++i) {
+      const long long r = static_cast<long long>(s0 + i) * rows + row;
+      const float w = expf(lse_accum[r] - total);
+      const floatx4* op = reinterpret_cast<const floatx4*>(o_accum + r * kDv + lane * 8);
+      floatx4 a = op[0], c = op[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] += w * a[j];
+        acc[4 + j] += w * c[j];
+      }
+    }
+  }
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = static_cast<bf16>(acc[j]);
+  *reinterpret_cast<bf16x8*>(orow) = v;
+  if (lane == 0) *lse_out = total;
+}
+
+}  // namespace
+}  // namespace fa
+
+extern "C" int fa_mla_combine(const fa_mla_decode_args* a, void* stream) {
+  FA_CHECK_ARG(a != nullptr, "args is NULL");
+  FA_CHECK_ARG(a->batch >= 1 && a->s_q >= 1 && a->h_q >= 1, "bad batch/s_q/h_q");
+  FA_CHECK_ARG(a->out && a->lse && a->o_accum && a->lse_accum && a->num_splits,
+               "NULL output/workspace pointer");
+  const int rows = a->s_q * a->h_q;
+  dim3 grid(fa::cdiv(rows, fa::kRowsPerBlock), a->batch);
+  hipLaunchKernelGGL(fa::mla_combine_kernel, grid, dim3(fa::kCombineThreads), 0,
+                     static_cast<hipStream_t>(stream), a->o_accum, a->lse_accum, a->num_splits,
+                     static_cast<fa::bf16*>(a->out), a->lse, a->s_q, a->h_q,
+                     a->batch + a->num_parts);
+  FA_CHECK_HIP(hipGetLastError());
+  return FA_OK;
+}

@@ -1,0 +1,585 @@
+// MLA decode kernels for gfx950: dense paged, sparse top-k bf16, sparse fp8.
+//
+// One work-group = 4 waves = 64 query rows (heads head0..head0+63 of query
+// token s) x one scheduler part (a run of 64-token KV tiles, possibly spanning
+// several sequences).  Per tile:
+//   * the 64 cache rows (576 bf16 each) are copied HBM -> LDS with
+//     global_load_lds_dwordx4 (no VGPR staging), double-buffered so the copy
+//     of tile i+1 overlaps the math of tile i;
+//   * QK^T on MFMA 32x32x16 bf16: wave (qh, qt) computes S^T for 32 tokens
+//     (qt) x 32 heads (qh); its Q^T operand (32 heads x 576) lives in VGPRs
+//     for the whole sequence;
+//   * online softmax in the log2 domain; the row max is combined across the
+//     two token halves through LDS, the row sum is kept per wave and summed
+//     once at the end;
+//   * P (bf16) goes through LDS; PV on MFMA: wave w owns value dims
+//     [128w, 128w+128) for all 64 heads, reading V^T operands straight from
+//     the row-major tile (V = first 512 dims of each cached row).
+// Unsplit sequences are normalised and written as bf16 out / fp32 lse;
+// split ones write fp32 (o, lse) partials for fa_mla_combine.
+//
+// Reference lineage: gather + online softmax of _paged_attn_kernel
+// (src/flag_attn/paged.py:296-337) and the per-split (o, lse) epilogue of
+// _fwd_split_kv_kernel (src/flag_attn/split_kv.py:161-174).
+#include "fa_common.h"
+
+namespace fa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowBytes = kDqk * 2;              // 1152 B: one bf16 cache row
+constexpr int kLdsRow = kRowBytes + 16;          // 1168 B: +16 B pad per row
+constexpr int kRowChunks = kLdsRow / 16;         // 73 16-byte chunks per LDS row
+constexpr int kDataChunks = kRowBytes / 16;      // 72 of them hold data
+constexpr int kTileBytes = kPage * kLdsRow;      // 74752 B per LDS tile
+constexpr int kLoadInsts = kPage * kRowChunks / 64;  // 73 wave-wide 1 KB copies
+constexpr int kPRow = kPage * 2 + 16;            // 144 B per P row (64 bf16 + pad)
+constexpr int kFp8RowBytes = FA_MLA_FP8_ROW_BYTES;  // 656
+constexpr int kQSteps = kDqk / 16;               // 36 MFMA k-steps for QK
+
+static_assert(kPage * kRowChunks % 64 == 0, "tile copy must be whole wave instructions");
+
+enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
+
+struct __attribute__((aligned(16))) Smem {
+  unsigned char kv[2][kTileBytes];   // double-buffered bf16 tiles
+  unsigned char p[kRows * kPRow];    // P as [head][token] bf16
+  float red[2][kRows];               // per token-half row maxima
+  float lsum[2][kRows];              // per token-half row sums (epilogue)
+  int32_t rows[4][kPage];            // sparse: physical row of each tile slot
+  unsigned long long vmask[4];       // sparse: valid-slot bitmask per tile
+};
+
+__device__ inline floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Load through the scalar unit (constant address space): for wave-uniform
+// metadata, so the value arrives via lgkmcnt and never forces a vmcnt wait on
+// the tile copies in flight.
+template <typename T>
+__device__ inline T sload(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
+__device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
+__device__ inline void barrier() {
+  wait_lds();
+  __builtin_amdgcn_s_barrier();
+}
+
+__device__ inline void copy16_to_lds(const unsigned char* src, unsigned char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                   (FA_LDS void*)(lds_wave_base), 16, 0, 0);
+}
+
+// Issue the copy of one 64-row bf16 tile into an LDS buffer.  `row_addr(r)`
+// gives the global address of tile row r, or nullptr for a row that must be
+// zero-filled (beyond the sequence / masked slot).
+template <typename RowAddr>
+__device__ inline void issue_tile_bf16(unsigned char* buf, RowAddr row_addr) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int j = wave; j < kLoadInsts; j += 4) {
+    const int q = 64 * j + lane;
+    const int row = q / kRowChunks;
+    const int col = q - row * kRowChunks;
+    unsigned char* base = buf + 64 * 16 * j;  // wave-uniform LDS destination
+    if (col < kDataChunks) {
+      const unsigned char* src = row_addr(row);
+      if (src != nullptr) {
+        copy16_to_lds(src + 16 * col, base);
+      } else {
+        *reinterpret_cast<uintx4*>(base + 16 * lane) = uintx4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+}
+
+// fp8-e4m3 (OCP "fn") pair -> two floats, using the gfx950 converter.
+template <bool kHi>
+__device__ inline floatx2 fp8x2_to_f32(unsigned int word) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8(word, kHi);
+}
+
+// Raw fp8 row slice held by one thread: (row r, quarter qd) -> 128 latent
+// codes, their fp32 scale and 16 rope dims.
+struct Fp8Slice {
+  uintx4 code[8];
+  float scale;
+  uintx4 rope[2];
+  bool valid;
+};
+
+__device__ inline void load_fp8_slice(Fp8Slice& f, const unsigned char* row, int qd) {
+  f.valid = row != nullptr;
+  if (!f.valid) return;
+  const uintx4* c = reinterpret_cast<const uintx4*>(row + 128 * qd);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f.code[i] = c[i];
+  f.scale = *reinterpret_cast<const float*>(row + 512 + 4 * qd);
+  const uintx4* r = reinterpret_cast<const uintx4*>(row + 528 + 32 * qd);
+  f.rope[0] = r[0];
+  f.rope[1] = r[1];
+}
+
+__device__ inline unsigned int pack_bf16x2(float a, float b) {
+  bf16 x = static_cast<bf16>(a), y = static_cast<bf16>(b);
+  return static_cast<unsigned int>(__builtin_bit_cast(unsigned short, x)) |
+         (static_cast<unsigned int>(__builtin_bit_cast(unsigned short, y)) << 16);
+}
+
+// Dequantise a thread's fp8 slice into the bf16 LDS tile (row r, dims
+// [128 qd, 128 qd + 128) and rope dims [512 + 16 qd, 512 + 16 qd + 16)).
+__device__ inline void store_fp8_slice(unsigned char* buf, const Fp8Slice& f, int r, int qd) {
+  uintx4* dst = reinterpret_cast<uintx4*>(buf + r * kLdsRow + 256 * qd);
+  uintx4* rdst = reinterpret_cast<uintx4*>(buf + r * kLdsRow + 1024 + 32 * qd);
+  if (!f.valid) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dst[i] = uintx4{0u, 0u, 0u, 0u};
+    rdst[0] = uintx4{0u, 0u, 0u, 0u};
+    rdst[1] = uintx4{0u, 0u, 0u, 0u};
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    // 16 codes -> 16 bf16 = two 16-byte LDS chunks
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned int w0 = f.code[i][2 * h], w1 = f.code[i][2 * h + 1];
+      floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
+      floatx2 c = fp8x2_to_f32<false>(w1), d = fp8x2_to_f32<true>(w1);
+      uintx4 o;
+      o[0] = pack_bf16x2(a[0] * f.scale, a[1] * f.scale);
+      o[1] = pack_bf16x2(b[0] * f.scale, b[1] * f.scale);
+      o[2] = pack_bf16x2(c[0] * f.scale, c[1] * f.scale);
+      o[3] = pack_bf16x2(d[0] * f.scale, d[1] * f.scale);
+      dst[2 * i + h] = o;
+    }
+  }
+  rdst[0] = f.rope[0];
+  rdst[1] = f.rope[1];
+}
+
+template <int kMode>
+__global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_decode_args a,
+                                                                 int num_m_blocks, int htiles) {
+  __shared__ Smem sm;
+
+  // XCD-aware work-group -> (part, m-block): work-groups are dealt round-robin
+  // over the 8 XCDs, so the m-blocks of one part share an XCD (and its L2)
+  // and read each KV tile from HBM once.
+  const int wg = blockIdx.x;
+  int part, mb;
+  if ((a.num_parts & 7) == 0) {
+    const int x = wg & 7, k = wg >> 3;
+    mb = k % num_m_blocks;
+    part = (k / num_m_blocks) * 8 + x;
+  } else {
+    part = wg / num_m_blocks;
+    mb = wg - part * num_m_blocks;
+  }
+  const int32_t* md = a.tile_md + part * kMdStride;
+  const int nblocks_part = sload(md + 5);
+  if (nblocks_part == 0) return;
+  const int b_begin = sload(md + 0), blk_begin = sload(md + 1);
+  const int b_end = sload(md + 2), blk_end = sload(md + 3);
+  const int first_local = sload(md + 4);
+
+  const int s = mb / htiles;
+  const int head0 = (mb - s * htiles) * kRows;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, li = lane & 31;
+  const int qh = wave & 1, qt = wave >> 1;
+  const float scale_log2 = a.softmax_scale * kLog2e;
+  const float ninf = -__builtin_inff();
+  const int topk_pad = (a.topk + kPage - 1) / kPage * kPage;
+
+  const unsigned char* kv = static_cast<const unsigned char*>(a.kv);
+  const bf16* q = static_cast<const bf16*>(a.q);
+
+  // Metadata from another batch / topk must not drive accesses out of bounds:
+  // sequence, block and split indices are clamped to this call's shapes.
+  const int b_last = b_end < a.batch ? b_end : a.batch - 1;
+  const int max_split = a.batch + a.num_parts;
+  for (int b = b_begin < 0 ? 0 : b_begin; b <= b_last; ++b) {
+    const int seqlen = sload(a.cache_seqlens + b);
+    const int nblk_seq = (kMode == kDense) ? (seqlen > 0 ? (seqlen + kPage - 1) / kPage : 0)
+                                           : topk_pad / kPage;
+    const int blk_lo = (b == b_begin) ? blk_begin : 0;
+    const int blk_hi = (b == b_end && blk_end < nblk_seq) ? blk_end : nblk_seq;
+    if (blk_lo < 0 || blk_hi <= blk_lo) continue;
+    const int ntiles = blk_hi - blk_lo;
+    const int split_local = (b == b_begin) ? first_local : 0;
+    const int ns0 = sload(a.num_splits + b);
+    const int nsplit = sload(a.num_splits + b + 1) - ns0;
+    const bool split_ok = ns0 >= 0 && split_local >= 0 && ns0 + split_local < max_split;
+    // keys visible to this m-block's query token (dense; bottom-right causal)
+    const int limit = (kMode == kDense && a.causal) ? seqlen - a.s_q + 1 + s : seqlen;
+    const int32_t* bt = a.block_table + static_cast<long long>(b) * a.bt_stride_b;
+    const int32_t* srows =
+        kMode == kDense ? nullptr
+                        : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s) * topk_pad;
+
+    // ---- Q^T operand: 32 heads x 576 dims in VGPRs ----
+    bf16x8 qf[kQSteps];
+    {
+      const int head = head0 + 32 * qh + li;
+      if (head < a.h_q) {
+        const bf16* qrow = q + b * a.q_stride_b + s * a.q_stride_s + head * a.q_stride_h + 8 * g;
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) qf[k] = *reinterpret_cast<const bf16x8*>(qrow + 16 * k);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) qf[k] = bf16x8{};
+      }
+    }
+
+    // ---- tile producers ----
+    // Data of tile t is requested kAhead iterations before it is used: bf16
+    // tiles go straight to LDS (kAhead = 1); fp8 tiles are staged in VGPRs
+    // and dequantised into LDS one iteration later (kAhead = 2).  Sparse row
+    // lists are published to LDS one iteration before their data request.
+    constexpr int kAhead = kMode == kSparseFp8 ? 2 : 1;
+    int32_t next_rows = -1;  // sparse: wave 0's copy of a future tile's rows
+    Fp8Slice f8;
+    const int f8_r = tid >> 2, f8_qd = tid & 3;
+    int next_phys = 0;  // dense: page of the next tile to request
+
+    auto sparse_row_ptr = [&](int32_t row) -> const unsigned char* {
+      if (row < 0) return nullptr;
+      return kv + static_cast<long long>(row >> 6) * a.kv_block_stride +
+             static_cast<long long>(row & 63) * a.kv_row_stride;
+    };
+    auto publish_rows = [&](int t, int32_t rowv) {  // rows of tile t -> slot t % 4
+      if (wave == 0) {
+        sm.rows[t & 3][lane] = rowv;
+        const unsigned long long m = __ballot(rowv >= 0);
+        if (lane == 0) sm.vmask[t & 3] = m;
+      }
+    };
+    auto load_rows = [&](int t) -> int32_t {
+      if (wave != 0 || t >= ntiles) return -1;
+      return srows[(blk_lo + t) * kPage + lane];
+    };
+    auto issue = [&](int t) {  // request the data of tile t into LDS buffer t & 1
+      unsigned char* buf = sm.kv[t & 1];
+      if constexpr (kMode == kDense) {
+        // A page id outside the cache (or a block beyond the table) is read
+        // as an all-masked page instead of faulting.
+        const int blk = blk_lo + t;
+        const bool page_ok =
+            blk < a.max_blocks_per_seq && next_phys >= 0 && next_phys < a.num_kv_blocks;
+        const int valid_rows = page_ok ? seqlen - blk * kPage : 0;
+        const unsigned char* page = kv + static_cast<long long>(next_phys) * a.kv_block_stride;
+        issue_tile_bf16(buf, [&](int r) -> const unsigned char* {
+          return r < valid_rows ? page + static_cast<long long>(r) * a.kv_row_stride : nullptr;
+        });
+        if (tid == 0) {
+          const int lim = limit - blk * kPage;
+          sm.vmask[t & 3] = !page_ok || lim <= 0 ? 0ull
+                            : lim >= 64          ? ~0ull
+                                                 : ((1ull << lim) - 1ull);
+        }
+        next_phys = (t + 1 < ntiles && blk + 1 < a.max_blocks_per_seq) ? sload(bt + blk + 1) : -1;
+      } else if constexpr (kMode == kSparseBf16) {
+        const int32_t* rr = sm.rows[t & 3];
+        issue_tile_bf16(buf, [&](int r) { return sparse_row_ptr(rr[r]); });
+      } else {
+        load_fp8_slice(f8, sparse_row_ptr(sm.rows[t & 3][f8_r]), f8_qd);
+      }
+    };
+
+    // ---- prologue ----
+    if constexpr (kMode != kDense) {
+      for (int t = 0; t <= kAhead; ++t) publish_rows(t, load_rows(t));
+      next_rows = load_rows(kAhead + 1);
+      barrier();
+    } else {
+      next_phys = blk_lo < a.max_blocks_per_seq ? sload(bt + blk_lo) : -1;
+    }
+    issue(0);
+    if constexpr (kMode == kSparseFp8) {
+      wait_vmem();
+      store_fp8_slice(sm.kv[0], f8, f8_r, f8_qd);
+      if (ntiles > 1) issue(1);
+    }
+
+    // Online softmax state, log2 units.  mref is the reference max that P and
+    // the accumulators are relative to; it is raised only when a tile max
+    // exceeds it by more than kSlack, so most tiles skip the rescale (P stays
+    // <= 2^kSlack, far inside fp32 / bf16 range).
+    float mref0 = ninf, mref1 = ninf;  // heads li and 32+li of this m-block
+    float lpart = 0.f;                 // row sum of head 32qh+li over my tokens
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i][0] = floatx16{};
+      acc[i][1] = floatx16{};
+    }
+
+    for (int it = 0; it < ntiles; ++it) {
+      const int blk = blk_lo + it;
+      const unsigned char* kvb = sm.kv[it & 1];
+      wait_vmem();
+      barrier();  // tile it resident; everyone done with tile it-1
+      if constexpr (kMode == kSparseFp8) {
+        if (it + 1 < ntiles) store_fp8_slice(sm.kv[(it + 1) & 1], f8, f8_r, f8_qd);
+      }
+      if (it + kAhead < ntiles) issue(it + kAhead);
+      if constexpr (kMode != kDense) {
+        publish_rows(it + kAhead + 1, next_rows);
+        next_rows = load_rows(it + kAhead + 2);
+      }
+
+      // ---- S^T = K Q^T for 32 tokens x 32 heads ----
+      floatx16 sacc = floatx16{};
+      {
+        const unsigned char* arow = kvb + (32 * qt + li) * kLdsRow + 16 * g;
+        constexpr int kPre = 4;
+        bf16x8 af[kPre];
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) af[k] = *reinterpret_cast<const bf16x8*>(arow + 32 * k);
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) {
+          const bf16x8 cur = af[k % kPre];
+          if (k + kPre < kQSteps)
+            af[k % kPre] = *reinterpret_cast<const bf16x8*>(arow + 32 * (k + kPre));
+          sacc = mfma32(cur, qf[k], sacc);
+        }
+      }
+
+      // ---- mask, scale, tile row max ----
+      const unsigned long long valid = sm.vmask[it & 3];
+      float sv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sv[r] = sacc[r] * scale_log2;
+      if (valid != ~0ull) {  // partial tile (uniform branch)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tok = 32 * qt + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (!((valid >> tok) & 1ull)) sv[r] = ninf;
+        }
+      }
+      float mloc = sv[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, sv[r]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      if (g == 0) sm.red[qt][32 * qh + li] = mloc;
+      barrier();
+
+      const float t0 = fmaxf(sm.red[0][li], sm.red[1][li]);
+      const float t1 = fmaxf(sm.red[0][32 + li], sm.red[1][32 + li]);
+      constexpr float kSlack = 8.f;
+      const bool up0 = t0 > mref0 + kSlack || (mref0 == ninf && t0 != ninf);
+      const bool up1 = t1 > mref1 + kSlack || (mref1 == ninf && t1 != ninf);
+      float al0 = 1.f, al1 = 1.f;
+      if (up0) {
+        al0 = exp2f(mref0 - t0);
+        mref0 = t0;
+      }
+      if (up1) {
+        al1 = exp2f(mref1 - t1);
+        mref1 = t1;
+      }
+      const float mref = qh ? mref1 : mref0;
+      const float mu = mref == ninf ? 0.f : mref;
+
+      // ---- P = exp2(S - mref) -> LDS as [head][token] bf16 ----
+      {
+        float psum = 0.f;
+        unsigned char* prow = sm.p + (32 * qh + li) * kPRow + (32 * qt + 4 * g) * 2;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          float p0 = exp2f(sv[4 * qd + 0] - mu), p1 = exp2f(sv[4 * qd + 1] - mu);
+          float p2 = exp2f(sv[4 * qd + 2] - mu), p3 = exp2f(sv[4 * qd + 3] - mu);
+          psum += (p0 + p1) + (p2 + p3);
+          uintx2 w;
+          w[0] = pack_bf16x2(p0, p1);
+          w[1] = pack_bf16x2(p2, p3);
+          *reinterpret_cast<uintx2*>(prow + 16 * qd) = w;
+        }
+        lpart = lpart * (qh ? al1 : al0) + psum;
+      }
+      if (__any(up0 || up1)) {  // rare after the first tile
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i][0] *= al0;
+          acc[i][1] *= al1;
+        }
+      }
+      barrier();
+
+      // ---- O^T[128 dims x 64 heads] += V^T P^T ----
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 bp0 =
+            *reinterpret_cast<const bf16x8*>(sm.p + li * kPRow + (16 * kk + 8 * g) * 2);
+        const bf16x8 bp1 =
+            *reinterpret_cast<const bf16x8*>(sm.p + (32 + li) * kPRow + (16 * kk + 8 * g) * 2);
+        const unsigned short* vcol = reinterpret_cast<const unsigned short*>(
+                                         kvb + (16 * kk + 8 * g) * kLdsRow) +
+                                     128 * wave + li;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          ushortx8 va;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) va[c] = vcol[c * (kLdsRow / 2) + 32 * mt];
+          const bf16x8 av = __builtin_bit_cast(bf16x8, va);
+          acc[mt][0] = mfma32(av, bp0, acc[mt][0]);
+          acc[mt][1] = mfma32(av, bp1, acc[mt][1]);
+        }
+      }
+    }
+
+    // ---- epilogue: row sums, normalise, write out / partials ----
+    lpart += __shfl_xor(lpart, 32);
+    if (g == 0) sm.lsum[qt][32 * qh + li] = lpart;
+    barrier();
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int head = head0 + 32 * nt + li;
+      if (head >= a.h_q) continue;
+      const float l = sm.lsum[0][32 * nt + li] + sm.lsum[1][32 * nt + li];
+      const float m = nt ? mref1 : mref0;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float lse_v = l > 0.f ? (m + log2f(l)) * kLn2 : ninf;
+      const int dim0 = 128 * wave + 4 * g;
+      if (nsplit == 1) {
+        bf16* orow = static_cast<bf16*>(a.out) +
+                     ((static_cast<long long>(b) * a.s_q + s) * a.h_q + head) * kDv + dim0;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            uintx2 w;
+            w[0] = pack_bf16x2(acc[mt][nt][4 * qd + 0] * inv, acc[mt][nt][4 * qd + 1] * inv);
+            w[1] = pack_bf16x2(acc[mt][nt][4 * qd + 2] * inv, acc[mt][nt][4 * qd + 3] * inv);
+            *reinterpret_cast<uintx2*>(orow + 32 * mt + 8 * qd) = w;
+          }
+        if (wave == 0 && g == 0)
+          a.lse[(static_cast<long long>(b) * a.h_q + head) * a.s_q + s] = lse_v;
+      } else if (split_ok) {
+        const long long prow =
+            static_cast<long long>(ns0 + split_local) * (a.s_q * a.h_q) + s * a.h_q + head;
+        float* orow = a.o_accum + prow * kDv + dim0;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            floatx4 w;
+            w[0] = acc[mt][nt][4 * qd + 0] * inv;
+            w[1] = acc[mt][nt][4 * qd + 1] * inv;
+            w[2] = acc[mt][nt][4 * qd + 2] * inv;
+            w[3] = acc[mt][nt][4 * qd + 3] * inv;
+            *reinterpret_cast<floatx4*>(orow + 32 * mt + 8 * qd) = w;
+          }
+        if (wave == 0 && g == 0) a.lse_accum[prow] = lse_v;
+      }
+    }
+    barrier();  // LDS (tiles, lsum) is reused by the next sequence
+  }
+}
+
+// Sparse index translation: rows[b][s][j] = physical cache row of
+// indices[b][s][j] (block_table[b][i / 64] * 64 + i % 64), or -1 when the
+// slot is unused (j >= topk, i < 0 or i >= cache_seqlens[b]).
+__global__ __launch_bounds__(256) void mla_sparse_rows_kernel(const fa_mla_decode_args a,
+                                                              int32_t* __restrict__ rows,
+                                                              int topk_pad) {
+  const long long n = static_cast<long long>(a.batch) * a.s_q * topk_pad;
+  for (long long e = blockIdx.x * 256ll + threadIdx.x; e < n; e += 256ll * gridDim.x) {
+    const int j = static_cast<int>(e % topk_pad);
+    const long long bs = e / topk_pad;
+    const int s = static_cast<int>(bs % a.s_q);
+    const int b = static_cast<int>(bs / a.s_q);
+    int32_t out = -1;
+    if (j < a.topk) {
+      const int idx = a.indices[b * a.idx_stride_b + s * a.idx_stride_s + j];
+      if (idx >= 0 && idx < a.cache_seqlens[b] && (idx >> 6) < a.max_blocks_per_seq) {
+        const int32_t blk = a.block_table[b * a.bt_stride_b + (idx >> 6)];
+        // a page id outside the cache masks the slot instead of faulting
+        if (blk >= 0 && blk < a.num_kv_blocks) out = blk * kPage + (idx & 63);
+      }
+    }
+    rows[e] = out;
+  }
+}
+
+int check_common(const fa_mla_decode_args* a) {
+  FA_CHECK_ARG(a != nullptr, "args is NULL");
+  FA_CHECK_ARG(a->batch >= 1 && a->batch <= FA_MLA_MAX_BATCH, "batch %d outside [1, %d]",
+               a->batch, FA_MLA_MAX_BATCH);
+  FA_CHECK_ARG(a->s_q >= 1 && a->h_q >= 1, "s_q %d / h_q %d must be >= 1", a->s_q, a->h_q);
+  FA_CHECK_ARG(a->num_parts >= 1 && a->num_parts <= FA_MLA_MAX_PARTS, "num_parts %d invalid",
+               a->num_parts);
+  FA_CHECK_ARG(a->q && a->kv && a->block_table && a->cache_seqlens && a->tile_md &&
+                   a->num_splits && a->out && a->lse && a->o_accum && a->lse_accum,
+               "NULL tensor pointer");
+  FA_CHECK_ARG((reinterpret_cast<uintptr_t>(a->q) & 15) == 0 && (a->q_stride_h % 8) == 0 &&
+                   (a->q_stride_s % 8) == 0 && (a->q_stride_b % 8) == 0,
+               "q rows must be 16-byte aligned");
+  FA_CHECK_ARG((reinterpret_cast<uintptr_t>(a->kv) & 15) == 0 && (a->kv_block_stride % 16) == 0 &&
+                   (a->kv_row_stride % 16) == 0,
+               "kv cache rows must be 16-byte aligned");
+  return FA_OK;
+}
+
+template <int kMode>
+int launch_decode(const fa_mla_decode_args* a, hipStream_t stream) {
+  const int htiles = cdiv(a->h_q, kRows);
+  const int num_m_blocks = a->s_q * htiles;
+  const int grid = a->num_parts * num_m_blocks;
+  hipLaunchKernelGGL(mla_decode_kernel<kMode>, dim3(grid), dim3(kThreads), 0, stream, *a,
+                     num_m_blocks, htiles);
+  FA_CHECK_HIP(hipGetLastError());
+  return FA_OK;
+}
+
+}  // namespace
+}  // namespace fa
+
+extern "C" int fa_mla_decode_dense(const fa_mla_decode_args* a, void* stream) {
+  int rc = fa::check_common(a);
+  if (rc != FA_OK) return rc;
+  FA_CHECK_ARG(a->kv_row_stride >= 2 * fa::kDqk, "kv_row_stride %lld < 1152",
+               static_cast<long long>(a->kv_row_stride));
+  return fa::launch_decode<fa::kDense>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fa_mla_sparse_rows(const fa_mla_decode_args* a, void* stream) {
+  FA_CHECK_ARG(a != nullptr, "args is NULL");
+  FA_CHECK_ARG(a->batch >= 1 && a->batch <= FA_MLA_MAX_BATCH && a->s_q >= 1,
+               "batch %d / s_q %d invalid", a->batch, a->s_q);
+  FA_CHECK_ARG(a->indices && a->sparse_rows && a->block_table && a->cache_seqlens,
+               "indices / sparse_rows / block_table / cache_seqlens is NULL");
+  FA_CHECK_ARG(a->topk >= 1, "topk %d < 1", a->topk);
+  FA_CHECK_ARG(a->num_kv_blocks >= 1, "num_kv_blocks %lld < 1",
+               static_cast<long long>(a->num_kv_blocks));
+  const int topk_pad = fa::cdiv(a->topk, fa::kPage) * fa::kPage;
+  const long long n = static_cast<long long>(a->batch) * a->s_q * topk_pad;
+  const long long want = (n + 255) / 256;
+  const int grid = static_cast<int>(want < 4096 ? want : 4096);
+  hipLaunchKernelGGL(fa::mla_sparse_rows_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *a, a->sparse_rows, topk_pad);
+  FA_CHECK_HIP(hipGetLastError());
+  return FA_OK;
+}
+
+extern "C" int fa_mla_decode_sparse(const fa_mla_decode_args* a, int32_t fp8, void* stream) {
+  int rc = fa::check_common(a);
+  if (rc != FA_OK) return rc;
+  FA_CHECK_ARG(a->sparse_rows != nullptr, "sparse decode needs sparse_rows (fa_mla_sparse_rows)");
+  FA_CHECK_ARG(a->topk >= 1, "topk %d < 1", a->topk);
+  FA_CHECK_ARG(!a->causal, "causal masking does not apply to sparse decode");
+  if (fp8) {
+    FA_CHECK_ARG(a->kv_row_stride >= fa::kFp8RowBytes, "fp8 kv_row_stride %lld < 656",
+                 static_cast<long long>(a->kv_row_stride));
+    return fa::launch_decode<fa::kSparseFp8>(a, static_cast<hipStream_t>(stream));
+  }
+  FA_CHECK_ARG(a->kv_row_stride >= 2 * fa::kDqk, "kv_row_stride %lld < 1152",
+               static_cast<long long>(a->kv_row_stride));
+  return fa::launch_decode<fa::kSparseBf16>(a, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,169 @@
+/*
+ * flagattention_amd.h -- C ABI of the MI355X (gfx950) MLA decode library
+ * (libflagattention_amd.so).
+ *
+ * Plain C: pointers, sizes and strides only.  No torch or HIP types cross
+ * this boundary; `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream).  The caller owns every buffer: the library never allocates or
+ * frees device memory and never synchronises the host.  Every call returns
+ * FA_OK (0) or a negative FA_ERR_* code; fa_last_error() then holds a
+ * message for the calling thread.
+ *
+ * The reference (FlagAttention) exposes its decode path as Python functions
+ * that launch Triton kernels, so there is no reference C symbol to mirror.
+ * Each entry point below replaces the kernel launch(es) of one reference
+ * decode stage; the Python host layer (flagattention_amd/mla.py) keeps the
+ * reference's operator conventions on top of it.
+ */
+#ifndef FLAGATTENTION_AMD_H
+#define FLAGATTENTION_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+#define FA_OK 0
+#define FA_ERR_INVALID_ARG (-1) /* shape / size / pointer check failed   */
+#define FA_ERR_HIP (-2)         /* a HIP runtime call failed             */
+#define FA_ERR_UNSUPPORTED (-3) /* valid request outside built variants  */
+
+/* Fixed geometry of the latent KV layout (DeepSeek-style MLA). */
+#define FA_MLA_PAGE_SIZE 64  /* tokens per KV page (block_size)          */
+#define FA_MLA_D_QK 576      /* 512 latent + 64 rope                     */
+#define FA_MLA_D_V 512       /* value = first 512 latent dims            */
+#define FA_MLA_ROWS_PER_TILE 64  /* query rows (heads) per work-group    */
+#define FA_MLA_MD_STRIDE 8   /* int32 words per tile-scheduler entry     */
+#define FA_MLA_FP8_ROW_BYTES 656 /* 512 e4m3 + 4 fp32 scales + 64 bf16   */
+#define FA_MLA_MAX_BATCH 4096
+#define FA_MLA_MAX_PARTS 1024
+
+/* Version of this ABI (FA_ABI_VERSION of the built library). */
+int fa_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* fa_last_error(void);
+
+/* Number of compute units of `device` (hipDeviceAttributeMultiprocessorCount). */
+int fa_device_cu_count(int device, int32_t* cu_count);
+
+/* sizeof(fa_mla_decode_args) as compiled into the library, so a binding can
+ * verify its mirror of the struct (Python: ctypes) before the first call. */
+int64_t fa_mla_decode_args_size(void);
+
+/*
+ * Tile-scheduler metadata: balanced split-KV partition of all sequences'
+ * 64-token blocks over `num_parts` work-group slots.
+ *
+ * Replaces the per-launch split heuristics of the reference,
+ * src/flag_attn/paged.py:52-67 (num_splits / partition_size) and
+ * src/flag_attn/split_kv.py:248-276 (num_splits_herustic), which pick one
+ * uniform split count per launch.  Here each part gets an equal share of
+ * (blocks + fixed_overhead per sequence) and sequences are cut wherever a
+ * share ends.
+ *
+ *   cache_seqlens  device int32[batch]; ignored when topk > 0
+ *   topk           > 0: sparse decode, every sequence has ceil(topk/64) blocks
+ *   fixed_overhead cost, in blocks, charged per sequence (>= 0)
+ *   tile_md        device int32[num_parts][8] (out):
+ *                    {begin_batch, begin_block, end_batch, end_block (excl.),
+ *                     first_split_local, num_blocks, begin_global_block, 0}
+ *   num_splits     device int32[batch+1] (out): exclusive prefix sum of the
+ *                  number of non-empty segments of each sequence
+ */
+int fa_mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, int32_t topk,
+                        int32_t num_parts, int32_t fixed_overhead, int32_t* tile_md,
+                        int32_t* num_splits, void* stream);
+
+/*
+ * Arguments of one MLA decode call.  Element strides are in elements of the
+ * tensor's own dtype; `kv_*_stride` are in BYTES.  The last dimension of
+ * q / kv rows is contiguous.
+ */
+typedef struct fa_mla_decode_args {
+  /* q: bf16 [batch][s_q][h_q][576] */
+  const void* q;
+  int64_t q_stride_b, q_stride_s, q_stride_h;
+  /* kv cache: [num_blocks][64][1][576] bf16 (row 1152 B) or
+   * [num_blocks][64][1][656] uint8 (fp8 row, 656 B) */
+  const void* kv;
+  int64_t kv_block_stride, kv_row_stride; /* bytes */
+  int64_t num_kv_blocks;
+  /* block_table: int32 [batch][max_blocks_per_seq] */
+  const int32_t* block_table;
+  int64_t bt_stride_b;
+  int32_t max_blocks_per_seq;
+  /* cache_seqlens: int32 [batch] */
+  const int32_t* cache_seqlens;
+  /* indices: int32 [batch][s_q][topk] logical token ids, -1 = unused (sparse) */
+  const int32_t* indices;
+  int64_t idx_stride_b, idx_stride_s;
+  int32_t topk;
+  /* sparse_rows: int32 [batch][s_q][topk_pad] physical cache rows written by
+   * fa_mla_sparse_rows (topk_pad = topk rounded up to 64); read by
+   * fa_mla_decode_sparse */
+  int32_t* sparse_rows;
+  /* scheduler metadata from fa_mla_get_metadata */
+  const int32_t* tile_md;
+  const int32_t* num_splits;
+  int32_t num_parts;
+  /* outputs: out bf16 [batch][s_q][h_q][512] contiguous,
+   *          lse fp32 [batch][h_q][s_q] contiguous */
+  void* out;
+  float* lse;
+  /* split workspace: o_accum fp32 [batch+num_parts][s_q*h_q][512],
+   *                  lse_accum fp32 [batch+num_parts][s_q*h_q] */
+  float* o_accum;
+  float* lse_accum;
+  int32_t batch, s_q, h_q;
+  float softmax_scale;
+  int32_t causal;
+} fa_mla_decode_args;
+
+/*
+ * Dense decode over the paged bf16 latent cache, writing final rows for
+ * unsplit sequences and (o, lse) partials for split ones.
+ * Replaces _paged_attn_kernel, src/flag_attn/paged.py:218-363 (gather via
+ * block_tables, online softmax) and _fwd_split_kv_kernel,
+ * src/flag_attn/split_kv.py:28-174 (per-split o and lse).
+ */
+int fa_mla_decode_dense(const fa_mla_decode_args* args, void* stream);
+
+/*
+ * Sparse index translation (gather addresses): writes args->sparse_rows,
+ *   rows[b][s][j] = block_table[b][i / 64] * 64 + i % 64,  i = indices[b][s][j]
+ * or -1 when j >= topk, i < 0 or i >= cache_seqlens[b].
+ * Same page arithmetic as the reference's gather, src/flag_attn/testing/
+ * paged.py:44-47 (block_table[j // block_size], j % block_size), applied to
+ * an index list instead of a contiguous range (the reference has no sparse
+ * path).
+ */
+int fa_mla_sparse_rows(const fa_mla_decode_args* args, void* stream);
+
+/*
+ * Sparse top-k decode: each query token attends only to the cache rows in
+ * args->sparse_rows (from fa_mla_sparse_rows); -1 rows are masked.
+ * fp8 != 0 selects the 656-byte fp8-e4m3 row layout (512 codes, 4 fp32
+ * per-128-dim scales, 64 bf16 rope dims; dequantised on chip), else the
+ * 1152-byte bf16 row.  No reference counterpart (the reference has no sparse
+ * path); writes outputs / partials under the same contract as the dense call.
+ */
+int fa_mla_decode_sparse(const fa_mla_decode_args* args, int32_t fp8, void* stream);
+
+/*
+ * LSE-weighted merge of split partials into out / lse for every sequence
+ * with more than one segment; sequences with no segment get out = 0,
+ * lse = -inf.  Replaces _fwd_combine_kv_splits,
+ * src/flag_attn/split_kv.py:176-241 (and _paged_attn_v2_reduce_kernel,
+ * src/flag_attn/paged.py:366-449).
+ */
+int fa_mla_combine(const fa_mla_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLAGATTENTION_AMD_H */

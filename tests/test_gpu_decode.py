@@ -1,0 +1,218 @@
+"""GPU parity of the HIP MLA decode path against the CPU oracle (MI355X only).
+
+Bars: scheduler metadata and sparse gather rows bit-exact; out within atol 2e-2 /
+rtol 1e-2 and lse within 1e-3 of the fp32 oracle (tolerances in tests/_helpers.py).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import flagattention_amd as fa
+from oracle import mla_oracle as orc
+from tests._helpers import DEV, assert_close, need_gpu, run_dense, run_sparse, say
+
+pytestmark = pytest.mark.gpu
+SCALE = 192 ** -0.5
+
+
+def _npz(golden_dir, name):
+    return np.load(os.path.join(golden_dir, name), allow_pickle=False)
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+# ---------------------------------------------------------------- metadata
+
+@pytest.mark.parametrize("lens,parts,topk", [
+    ([256, 384], 4, 0),
+    ([100, 0, 65], 1, 0),
+    ([64], 4, 0),
+    ([0, 0, 0], 8, 0),
+    ([5000] * 8, 16, 2048),
+    (list(range(0, 64 * 37, 37)), 128, 0),
+    ([4096 + (i * 977) % 4097 for i in range(64)], 128, 0),
+    ([128 * (1 + (i * 7919) % 512) for i in range(32)], 64, 0),
+    ([1 + (i * 31) % 100000 for i in range(1000)], 256, 0),
+])
+def test_metadata_kernel_matches_spec(lens, parts, topk):
+    need_gpu()
+    say(f"metadata lens={len(lens)} parts={parts} topk={topk}")
+    ld = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    md, ns = fa.get_mla_metadata(ld, 128, 1, topk=topk or None, num_sm_parts=parts)
+    torch.cuda.synchronize()
+    want_md, want_ns = orc.metadata_spec(lens, parts, fa.mla.FIXED_OVERHEAD_BLOCKS, topk)
+    assert md.cpu().tolist() == want_md
+    assert ns.cpu().tolist() == want_ns
+
+
+# ---------------------------------------------------------------- sparse gather rows
+
+def test_sparse_rows_golden_bit_exact(golden_dir):
+    need_gpu()
+    g = _npz(golden_dir, "sparse_bf16.npz")
+    rows = fa.sparse_rows(_t(g["indices"]).to(DEV), _t(g["block_table"]).to(DEV),
+                          _t(g["cache_seqlens"]).to(DEV), g["k_cache"].shape[0])
+    assert torch.equal(rows.cpu(), _t(g["rows"]))
+
+
+def test_sparse_rows_random_bit_exact():
+    need_gpu()
+    gen = torch.Generator().manual_seed(11)
+    lens = torch.tensor([3000, 70, 1, 9000], dtype=torch.int32)
+    bt = torch.randint(-2, 200, (4, 150), generator=gen, dtype=torch.int32)  # some bad pages
+    idx = torch.randint(-3, 9500, (4, 3, 1000), generator=gen, dtype=torch.int32)
+    rows = fa.sparse_rows(idx.to(DEV), bt.to(DEV), lens.to(DEV), 190)
+    assert torch.equal(rows.cpu(), orc.sparse_rows_ref(idx, bt, lens, 190))
+
+
+# ---------------------------------------------------------------- dense
+
+@pytest.mark.parametrize("name", ["dense_cfg1.npz", "dense_causal_sq2.npz"])
+@pytest.mark.parametrize("parts", [None, 1, 3])
+def test_dense_golden(golden_dir, name, parts):
+    need_gpu()
+    say(f"dense golden {name} parts={parts}")
+    g = _npz(golden_dir, name)
+    q = _t(g["q"]).to(torch.bfloat16)
+    kc = _t(g["k_cache"]).to(torch.bfloat16)
+    out, lse, _, _ = run_dense(q, kc, _t(g["block_table"]), _t(g["cache_seqlens"]),
+                               float(g["sm_scale"]), bool(g["causal"]), parts)
+    assert_close(out, lse, _t(g["out"]).float(), _t(g["lse"]).float())
+
+
+DENSE_CASES = [
+    # (batch, h_q, s_q, lens, causal, parts)
+    (2, 16, 1, [256, 384], False, None),
+    (6, 128, 1, [1, 63, 64, 65, 1000, 4097], False, None),
+    (6, 128, 1, [1, 63, 64, 65, 1000, 4097], False, 1),
+    (6, 128, 1, [1, 63, 64, 65, 1000, 4097], False, 37),
+    (4, 128, 2, [1, 2, 129, 3000], True, None),
+    (4, 128, 2, [1, 2, 129, 3000], True, 5),
+    (3, 64, 1, [0, 500, 0], False, None),
+    (3, 16, 2, [65, 7, 200], True, 2),
+    (2, 100, 1, [700, 300], False, None),  # h_q not a multiple of 64
+    (2, 128, 3, [190, 64], True, None),
+]
+
+
+@pytest.mark.parametrize("case", DENSE_CASES, ids=lambda c: f"B{c[0]}h{c[1]}s{c[2]}c{int(c[4])}p{c[5]}")
+def test_dense_random(case):
+    need_gpu()
+    batch, h_q, s_q, lens, causal, parts = case
+    say(f"dense random {case}")
+    q, kc, bt, ld = orc.make_dense_inputs(batch, h_q, s_q, lens, seed=sum(lens) + h_q,
+                                          scale=1.0, extra_blocks=3)
+    out, lse, _, _ = run_dense(q, kc, bt, ld, SCALE, causal, parts)
+    ref_out, ref_lse = orc.dense_decode_ref(q, kc, bt, ld, SCALE, causal)
+    assert_close(out, lse, ref_out, ref_lse)
+
+
+def test_dense_split_invariance():
+    """The same decode with 1 part (no split) and 128 parts (heavy splitting) agrees."""
+    need_gpu()
+    lens = [5000, 3000, 129, 64]
+    q, kc, bt, ld = orc.make_dense_inputs(4, 128, 1, lens, seed=5, scale=0.5)
+    o1, l1, _, ns1 = run_dense(q, kc, bt, ld, SCALE, False, 1)
+    o2, l2, _, ns2 = run_dense(q, kc, bt, ld, SCALE, False, 128)
+    assert ns1[-1] == 4 and ns2[-1] > 4
+    assert torch.allclose(o1.float(), o2.float(), atol=1e-2, rtol=1e-2)
+    assert torch.allclose(l1, l2, atol=1e-4)
+
+
+def test_dense_bad_page_is_masked_not_faulting():
+    """A block-table entry outside the cache reads as a masked page."""
+    need_gpu()
+    q, kc, bt, ld = orc.make_dense_inputs(1, 16, 1, [192], seed=9)
+    good = bt.clone()
+    bt[0, 1] = kc.shape[0] + 1000
+    out, lse, _, _ = run_dense(q, kc, bt, ld, SCALE)
+    keep = torch.cat([torch.arange(0, 64), torch.arange(128, 192)])
+    kv = orc.gather_rows(kc, good, 0, keep).float()
+    ref_o, ref_l = orc.attention_lse(q[0].float().permute(1, 0, 2), kv, kv[:, :512], SCALE, False)
+    assert_close(out, lse, ref_o.permute(1, 0, 2).unsqueeze(0), ref_l.unsqueeze(0))
+
+
+# ---------------------------------------------------------------- sparse
+
+@pytest.mark.parametrize("name,fp8", [("sparse_bf16.npz", False), ("sparse_fp8.npz", True)])
+def test_sparse_golden(golden_dir, name, fp8):
+    need_gpu()
+    say(f"sparse golden {name}")
+    g = _npz(golden_dir, name)
+    q = _t(g["q"]).to(torch.bfloat16)
+    kc = _t(g["k_cache"])
+    kc = kc if fp8 else kc.to(torch.bfloat16)
+    out, lse = run_sparse(q, kc, _t(g["block_table"]), _t(g["cache_seqlens"]),
+                          _t(g["indices"]), float(g["sm_scale"]), fp8)
+    assert_close(out, lse, _t(g["out"]).float(), _t(g["lse"]).float())
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("topk,parts", [(256, None), (2048, None), (100, 3), (2048, 1)])
+def test_sparse_random(fp8, topk, parts):
+    need_gpu()
+    say(f"sparse random fp8={fp8} topk={topk} parts={parts}")
+    lens = [5000, 2100, 3000]
+    q, kc, bt, ld = orc.make_dense_inputs(3, 128, 1, lens, seed=topk, scale=0.1, extra_blocks=2)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=topk + 1)
+    idx = orc.make_sparse_indices(3, 1, topk, lens, seed=topk + 2)
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8, parts)
+    ref_out, ref_lse = orc.sparse_decode_ref(q, kc, bt, ld, idx, SCALE, is_fp8=fp8)
+    assert_close(out, lse, ref_out, ref_lse)
+
+
+def test_sparse_all_masked_row():
+    need_gpu()
+    q, kc, bt, ld = orc.make_dense_inputs(2, 64, 1, [300, 300], seed=4)
+    idx = orc.make_sparse_indices(2, 1, 128, [300, 300], seed=5, invalid_frac=0.0)
+    idx[1] = -1
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE)
+    ref_out, ref_lse = orc.sparse_decode_ref(q, kc, bt, ld, idx, SCALE)
+    assert bool(torch.isneginf(lse[1]).all()) and bool((out[1] == 0).all())
+    assert_close(out, lse, ref_out, ref_lse)
+
+
+def test_fp8_codec_exhaustive():
+    """Every e4m3 code through the kernel's dequantiser, in K (lse) and V (out).
+
+    One valid key per query token makes P = 1, so out = bf16(code * scale) exactly and
+    lse = k[d] * sm_scale for a one-hot query at dim d.
+    """
+    need_gpu()
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes[0x7F] = 0
+    codes[0xFF] = 0  # the two NaN codes are not data
+    lat = torch.cat([codes, codes.flip(0)])
+    scales = torch.tensor([1.0, 2.0, 0.5, 0.015625], dtype=torch.float32)
+    rope = torch.linspace(-3, 3, 64).to(torch.bfloat16)
+    row = torch.cat([lat, scales.view(torch.uint8), rope.view(torch.uint8)])
+    kc = torch.zeros((2, 64, 1, 656), dtype=torch.uint8)
+    kc[1, 5, 0] = row
+    s_q, h_q = 5, 128
+    q = torch.zeros((1, s_q, h_q, 576), dtype=torch.bfloat16)
+    for s in range(s_q):
+        for h in range(h_q):
+            d = s * h_q + h
+            if d < 576:
+                q[0, s, h, d] = 1.0
+    bt = torch.tensor([[0, 1]], dtype=torch.int32)
+    lens = torch.tensor([128], dtype=torch.int32)
+    idx = torch.full((1, s_q, 64), -1, dtype=torch.int32)
+    idx[0, :, 17] = 64 + 5  # logical token 69 -> page 1 row 5
+    out, lse = run_sparse(q, kc, bt, lens, idx, 1.0, fp8=True)
+    dec = orc.fp8_rows_dequant(row.view(1, 656))[0]  # fp32 [576]
+    want_v = dec[:512].to(torch.bfloat16)
+    for s in range(s_q):
+        for h in range(h_q):
+            assert torch.equal(out[0, s, h], want_v), f"V dequant differs (s={s}, h={h})"
+    for s in range(s_q):
+        for h in range(h_q):
+            d = s * h_q + h
+            want = float(dec[d].to(torch.bfloat16)) if d < 576 else 0.0
+            assert abs(float(lse[0, h, s]) - want) <= 1e-6 * max(1.0, abs(want)), (s, h, d)
