@@ -7,16 +7,24 @@
 //     global_load_lds_dwordx4 (no VGPR staging), double-buffered so the copy
 //     of tile i+1 overlaps the math of tile i;
 //   * QK^T on MFMA 32x32x16 bf16: wave (qh, qt) computes S^T for 32 tokens
-//     (qt) x 32 heads (qh); its Q^T operand (32 heads x 576) lives in VGPRs
-//     for the whole sequence;
+//     (qt) x 32 heads (qh); its Q^T operand (32 heads x 576) lives in
+//     registers for the whole sequence;
 //   * online softmax in the log2 domain; the row max is combined across the
 //     two token halves through LDS, the row sum is kept per wave and summed
-//     once at the end;
+//     once at the end; the accumulators are rescaled only when the running
+//     max grows by more than 2^8;
 //   * P (bf16) goes through LDS; PV on MFMA: wave w owns value dims
-//     [128w, 128w+128) for all 64 heads, reading V^T operands straight from
-//     the row-major tile (V = first 512 dims of each cached row).
+//     [128w, 128w+128) for all 64 heads; its V^T operands are read from the
+//     row-major tile with ds_read_b64_tr_b16 (V = first 512 dims of a row).
 // Unsplit sequences are normalised and written as bf16 out / fp32 lse;
 // split ones write fp32 (o, lse) partials for fa_mla_combine.
+//
+// LDS tile layout: the 64 x 72 grid of 16-byte chunks (row r, logical chunk
+// k) is stored as 8 row-groups x 9 chunk-groups of 1 KB blocks.  Block
+// (r/8, k/8) holds slot (r%8)*8 + ((k%8) ^ swz(r)), swz(r) = (r&7)^((r>>3)&1).
+// One wave-wide global_load_lds fills exactly one block, so every copy lane
+// has a fixed source offset; the XOR keeps the QK operand reads (16 rows x
+// one chunk) free of bank conflicts.
 //
 // Reference lineage: gather + online softmax of _paged_attn_kernel
 // (src/flag_attn/paged.py:296-337) and the per-split (o, lse) epilogue of
@@ -27,28 +35,33 @@ namespace fa {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowBytes = kDqk * 2;              // 1152 B: one bf16 cache row
-constexpr int kLdsRow = kRowBytes + 16;          // 1168 B: +16 B pad per row
-constexpr int kRowChunks = kLdsRow / 16;         // 73 16-byte chunks per LDS row
-constexpr int kDataChunks = kRowBytes / 16;      // 72 of them hold data
-constexpr int kTileBytes = kPage * kLdsRow;      // 74752 B per LDS tile
-constexpr int kLoadInsts = kPage * kRowChunks / 64;  // 73 wave-wide 1 KB copies
-constexpr int kPRow = kPage * 2 + 16;            // 144 B per P row (64 bf16 + pad)
+constexpr int kRowBytes = kDqk * 2;          // 1152 B: one bf16 cache row
+constexpr int kChunkGroups = kRowBytes / 128;  // 9 groups of 8 chunks per row
+constexpr int kBlockBytes = 1024;            // 8 rows x 8 chunks
+constexpr int kRowGroupBytes = kChunkGroups * kBlockBytes;  // 9216
+constexpr int kTileBytes = kPage * kRowBytes;  // 73728 B per LDS tile
+constexpr int kPRow = kPage * 2 + 16;        // 144 B per P row (64 bf16 + pad)
 constexpr int kFp8RowBytes = FA_MLA_FP8_ROW_BYTES;  // 656
-constexpr int kQSteps = kDqk / 16;               // 36 MFMA k-steps for QK
-
-static_assert(kPage * kRowChunks % 64 == 0, "tile copy must be whole wave instructions");
+constexpr int kQSteps = kDqk / 16;           // 36 MFMA k-steps for QK
 
 enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 
 struct __attribute__((aligned(16))) Smem {
-  unsigned char kv[2][kTileBytes];   // double-buffered bf16 tiles
+  unsigned char kv[2][kTileBytes];   // double-buffered bf16 tiles (blocked layout)
   unsigned char p[kRows * kPRow];    // P as [head][token] bf16
   float red[2][kRows];               // per token-half row maxima
   float lsum[2][kRows];              // per token-half row sums (epilogue)
   int32_t rows[4][kPage];            // sparse: physical row of each tile slot
-  unsigned long long vmask[4];       // sparse: valid-slot bitmask per tile
+  unsigned long long vmask[4];       // valid-key bitmask per tile slot
 };
+
+__device__ inline int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Byte offset of (row r, logical 16-byte chunk k) in a tile.
+__device__ inline int tile_off(int r, int k) {
+  return ((r >> 3) * kChunkGroups + (k >> 3)) * kBlockBytes +
+         16 * (((r & 7) << 3) + ((k & 7) ^ swz(r)));
+}
 
 __device__ inline floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -69,29 +82,83 @@ __device__ inline void barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
-__device__ inline void copy16_to_lds(const unsigned char* src, unsigned char* lds_wave_base) {
+__device__ inline void copy16_to_lds(const unsigned char* src, unsigned char* lds_block) {
   __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                   (FA_LDS void*)(lds_wave_base), 16, 0, 0);
+                                   (FA_LDS void*)(lds_block), 16, 0, 0);
 }
 
-// Issue the copy of one 64-row bf16 tile into an LDS buffer.  `row_addr(r)`
-// gives the global address of tile row r, or nullptr for a row that must be
-// zero-filled (beyond the sequence / masked slot).
-template <typename RowAddr>
-__device__ inline void issue_tile_bf16(unsigned char* buf, RowAddr row_addr) {
+// LDS transpose read (ds_read_b64_tr_b16).  Within each 16-lane group, result
+// lane i, element e comes from source lane 4e + i/4, element i%4: four lanes
+// pointing at 4 consecutive dims of token row e give every lane one dim of 4
+// consecutive tokens (see the V^T operand addressing in the PV loop).
+__device__ inline bf16x4 lds_read_tr4(const unsigned char* p) {
+  typedef short shortx4 __attribute__((ext_vector_type(4)));
+  shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS shortx4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Copy this wave's 2 row-groups (16 rows) of a 64-row bf16 tile into LDS.
+// Lane i of block (R, G) moves row 8R + i/8, logical chunk 8G + ((i%8) ^
+// swz(8R + i/8)).
+//
+// Dense pages use buffer loads: the page is a scalar buffer resource whose
+// size is the page's valid bytes, so each copy is one 32-bit lane offset
+// (`voff[rl]`, fixed for the whole kernel) plus an immediate, and rows past
+// the end of the sequence (or a whole page that must not be read) come back
+// as zeros from the hardware range check instead of being fetched.
+// The immediate offset of an LDS-destination buffer load is added to the LDS
+// address as well as to the memory address, so the LDS base handed to the
+// instruction is pre-compensated by -128*G.
+template <int G>
+__device__ inline void copy_block_buf(__amdgpu_buffer_rsrc_t rs, unsigned char* dst,
+                                      unsigned int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (FA_LDS void*)(dst + G * (kBlockBytes - 128)), 16,
+                                           voff, 0, 128 * G, 0);
+}
+
+__device__ inline void copy_page_rows(unsigned char* buf, const unsigned char* page,
+                                      int valid_bytes, const unsigned int (&voff)[2]) {
+  const int wave = threadIdx.x >> 6;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(page), 0, valid_bytes,
+                                        0x00020000);
+#pragma unroll
+  for (int rl = 0; rl < 2; ++rl) {
+    unsigned char* dst = buf + (2 * wave + rl) * kRowGroupBytes;
+    copy_block_buf<0>(rs, dst, voff[rl]);
+    copy_block_buf<1>(rs, dst, voff[rl]);
+    copy_block_buf<2>(rs, dst, voff[rl]);
+    copy_block_buf<3>(rs, dst, voff[rl]);
+    copy_block_buf<4>(rs, dst, voff[rl]);
+    copy_block_buf<5>(rs, dst, voff[rl]);
+    copy_block_buf<6>(rs, dst, voff[rl]);
+    copy_block_buf<7>(rs, dst, voff[rl]);
+    copy_block_buf<8>(rs, dst, voff[rl]);
+  }
+}
+
+// Gathered rows (sparse): `rows[r]` is the physical cache row of tile row r
+// (-1: zero-fill).
+__device__ inline void copy_gather_rows(unsigned char* buf, const int32_t* rows,
+                                        const unsigned char* kv, long long block_stride,
+                                        long long row_stride) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int j = wave; j < kLoadInsts; j += 4) {
-    const int q = 64 * j + lane;
-    const int row = q / kRowChunks;
-    const int col = q - row * kRowChunks;
-    unsigned char* base = buf + 64 * 16 * j;  // wave-uniform LDS destination
-    if (col < kDataChunks) {
-      const unsigned char* src = row_addr(row);
-      if (src != nullptr) {
-        copy16_to_lds(src + 16 * col, base);
-      } else {
-        *reinterpret_cast<uintx4*>(base + 16 * lane) = uintx4{0u, 0u, 0u, 0u};
-      }
+  const int lrow = lane >> 3;
+#pragma unroll
+  for (int rl = 0; rl < 2; ++rl) {
+    const int R = 2 * wave + rl;
+    const int32_t row = rows[8 * R + lrow];
+    unsigned char* dst = buf + R * kRowGroupBytes;
+    if (row >= 0) {
+      const unsigned char* src = kv + static_cast<long long>(row >> 6) * block_stride +
+                                 static_cast<long long>(row & 63) * row_stride +
+                                 16 * ((lane & 7) ^ lrow ^ (R & 1));
+#pragma unroll
+      for (int G = 0; G < kChunkGroups; ++G) copy16_to_lds(src + 128 * G, dst + G * kBlockBytes);
+    } else {
+#pragma unroll
+      for (int G = 0; G < kChunkGroups; ++G)
+        *reinterpret_cast<uintx4*>(dst + G * kBlockBytes + 16 * lane) = uintx4{0u, 0u, 0u, 0u};
     }
   }
 }
@@ -129,23 +196,21 @@ __device__ inline unsigned int pack_bf16x2(float a, float b) {
          (static_cast<unsigned int>(__builtin_bit_cast(unsigned short, y)) << 16);
 }
 
-// Dequantise a thread's fp8 slice into the bf16 LDS tile (row r, dims
-// [128 qd, 128 qd + 128) and rope dims [512 + 16 qd, 512 + 16 qd + 16)).
+// Dequantise a thread's fp8 slice into the bf16 LDS tile: row r, logical
+// chunks [16 qd, 16 qd + 16) (dims 128 qd ..) and rope chunks 64 + 2 qd, +1.
 __device__ inline void store_fp8_slice(unsigned char* buf, const Fp8Slice& f, int r, int qd) {
-  uintx4* dst = reinterpret_cast<uintx4*>(buf + r * kLdsRow + 256 * qd);
-  uintx4* rdst = reinterpret_cast<uintx4*>(buf + r * kLdsRow + 1024 + 32 * qd);
   if (!f.valid) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dst[i] = uintx4{0u, 0u, 0u, 0u};
-    rdst[0] = uintx4{0u, 0u, 0u, 0u};
-    rdst[1] = uintx4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 16; ++i)
+      *reinterpret_cast<uintx4*>(buf + tile_off(r, 16 * qd + i)) = uintx4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<uintx4*>(buf + tile_off(r, 64 + 2 * qd)) = uintx4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<uintx4*>(buf + tile_off(r, 65 + 2 * qd)) = uintx4{0u, 0u, 0u, 0u};
     return;
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    // 16 codes -> 16 bf16 = two 16-byte LDS chunks
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 2; ++h) {  // 16 codes -> 16 bf16 = two 16-byte chunks
       const unsigned int w0 = f.code[i][2 * h], w1 = f.code[i][2 * h + 1];
       floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
       floatx2 c = fp8x2_to_f32<false>(w1), d = fp8x2_to_f32<true>(w1);
@@ -154,11 +219,11 @@ __device__ inline void store_fp8_slice(unsigned char* buf, const Fp8Slice& f, in
       o[1] = pack_bf16x2(b[0] * f.scale, b[1] * f.scale);
       o[2] = pack_bf16x2(c[0] * f.scale, c[1] * f.scale);
       o[3] = pack_bf16x2(d[0] * f.scale, d[1] * f.scale);
-      dst[2 * i + h] = o;
+      *reinterpret_cast<uintx4*>(buf + tile_off(r, 16 * qd + 2 * i + h)) = o;
     }
   }
-  rdst[0] = f.rope[0];
-  rdst[1] = f.rope[1];
+  *reinterpret_cast<uintx4*>(buf + tile_off(r, 64 + 2 * qd)) = f.rope[0];
+  *reinterpret_cast<uintx4*>(buf + tile_off(r, 65 + 2 * qd)) = f.rope[1];
 }
 
 template <int kMode>
@@ -200,6 +265,46 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
   const unsigned char* kv = static_cast<const unsigned char*>(a.kv);
   const bf16* q = static_cast<const bf16*>(a.q);
 
+  // Per-lane LDS offsets reused by every tile.
+  // QK A operand (token row 32qt+li, logical chunk 2k+g): 4 bases by k%4;
+  // k/4 selects the chunk-group block (+1 KB each).
+  int a_off[4];
+  {
+    const int r = 32 * qt + li;
+    const int base = (r >> 3) * kRowGroupBytes + 128 * (r & 7);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a_off[j] = base + 16 * ((2 * j + g) ^ swz(r));
+  }
+  // PV V^T operand via transpose reads: the 16-lane group (g, half16) reads
+  // token rows 16kk + 8g + 4h + c (c = (lane&15)>>2) at dims
+  // 128w + 32mt + 16 half16 + 4 qq (qq = lane&3).  Bases by (mt parity, h);
+  // kk adds two row-groups and mt/2 one chunk-group.
+  int v_off[2][2];
+  {
+    const int half16 = (lane >> 4) & 1, c = (lane & 15) >> 2, qq = lane & 3;
+#pragma unroll
+    for (int mp = 0; mp < 2; ++mp)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int rr = 4 * h + c;                        // token row in its row-group
+        const int kl = 4 * mp + 2 * half16 + (qq >> 1);  // logical chunk in its group
+        v_off[mp][h] = g * kRowGroupBytes + 2 * wave * kBlockBytes +
+                       16 * (rr * 8 + (kl ^ rr ^ g)) + 8 * (qq & 1);
+      }
+  }
+
+  // Dense copy lanes: byte offset of (row 8R + lane/8, chunk (lane%8)^swz) in a
+  // page for this wave's two row-groups R = 2*wave + rl.
+  unsigned int page_voff[2];
+  {
+    const int lrow = lane >> 3;
+#pragma unroll
+    for (int rl = 0; rl < 2; ++rl)
+      page_voff[rl] = static_cast<unsigned int>(
+          (8 * (2 * wave + rl) + lrow) * static_cast<int>(a.kv_row_stride) +
+          16 * ((lane & 7) ^ lrow ^ rl));
+  }
+
   // Metadata from another batch / topk must not drive accesses out of bounds:
   // sequence, block and split indices are clamped to this call's shapes.
   const int b_last = b_end < a.batch ? b_end : a.batch - 1;
@@ -223,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         kMode == kDense ? nullptr
                         : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s) * topk_pad;
 
-    // ---- Q^T operand: 32 heads x 576 dims in VGPRs ----
+    // ---- Q^T operand: 32 heads x 576 dims in registers ----
     bf16x8 qf[kQSteps];
     {
       const int head = head0 + 32 * qh + li;
@@ -272,21 +377,20 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         const int blk = blk_lo + t;
         const bool page_ok =
             blk < a.max_blocks_per_seq && next_phys >= 0 && next_phys < a.num_kv_blocks;
-        const int valid_rows = page_ok ? seqlen - blk * kPage : 0;
-        const unsigned char* page = kv + static_cast<long long>(next_phys) * a.kv_block_stride;
-        issue_tile_bf16(buf, [&](int r) -> const unsigned char* {
-          return r < valid_rows ? page + static_cast<long long>(r) * a.kv_row_stride : nullptr;
-        });
+        const int valid_rows = page_ok ? min(seqlen - blk * kPage, kPage) : 0;
+        const unsigned char* page = kv + static_cast<long long>(page_ok ? next_phys : 0) *
+                                             a.kv_block_stride;
+        copy_page_rows(buf, page, valid_rows * static_cast<int>(a.kv_row_stride), page_voff);
         if (tid == 0) {
           const int lim = limit - blk * kPage;
           sm.vmask[t & 3] = !page_ok || lim <= 0 ? 0ull
                             : lim >= 64          ? ~0ull
                                                  : ((1ull << lim) - 1ull);
         }
-        next_phys = (t + 1 < ntiles && blk + 1 < a.max_blocks_per_seq) ? sload(bt + blk + 1) : -1;
+        next_phys =
+            (t + 1 < ntiles && blk + 1 < a.max_blocks_per_seq) ? sload(bt + blk + 1) : -1;
       } else if constexpr (kMode == kSparseBf16) {
-        const int32_t* rr = sm.rows[t & 3];
-        issue_tile_bf16(buf, [&](int r) { return sparse_row_ptr(rr[r]); });
+        copy_gather_rows(buf, sm.rows[t & 3], kv, a.kv_block_stride, a.kv_row_stride);
       } else {
         load_fp8_slice(f8, sparse_row_ptr(sm.rows[t & 3][f8_r]), f8_qd);
       }
@@ -321,7 +425,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     }
 
     for (int it = 0; it < ntiles; ++it) {
-      const int blk = blk_lo + it;
       const unsigned char* kvb = sm.kv[it & 1];
       wait_vmem();
       barrier();  // tile it resident; everyone done with tile it-1
@@ -337,16 +440,19 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       // ---- S^T = K Q^T for 32 tokens x 32 heads ----
       floatx16 sacc = floatx16{};
       {
-        const unsigned char* arow = kvb + (32 * qt + li) * kLdsRow + 16 * g;
-        constexpr int kPre = 4;
+        constexpr int kPre = 6;
         bf16x8 af[kPre];
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) af[k] = *reinterpret_cast<const bf16x8*>(arow + 32 * k);
+        for (int k = 0; k < kPre; ++k)
+          af[k] = *reinterpret_cast<const bf16x8*>(kvb + a_off[k & 3] + (k >> 2) * kBlockBytes);
 #pragma unroll
         for (int k = 0; k < kQSteps; ++k) {
           const bf16x8 cur = af[k % kPre];
-          if (k + kPre < kQSteps)
-            af[k % kPre] = *reinterpret_cast<const bf16x8*>(arow + 32 * (k + kPre));
+          if (k + kPre < kQSteps) {
+            const int kn = k + kPre;
+            af[k % kPre] =
+                *reinterpret_cast<const bf16x8*>(kvb + a_off[kn & 3] + (kn >> 2) * kBlockBytes);
+          }
           sacc = mfma32(cur, qf[k], sacc);
         }
       }
@@ -419,15 +525,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             *reinterpret_cast<const bf16x8*>(sm.p + li * kPRow + (16 * kk + 8 * g) * 2);
         const bf16x8 bp1 =
             *reinterpret_cast<const bf16x8*>(sm.p + (32 + li) * kPRow + (16 * kk + 8 * g) * 2);
-        const unsigned short* vcol = reinterpret_cast<const unsigned short*>(
-                                         kvb + (16 * kk + 8 * g) * kLdsRow) +
-                                     128 * wave + li;
+        const unsigned char* vb = kvb + kk * 2 * kRowGroupBytes;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          ushortx8 va;
-#pragma unroll
-          for (int c = 0; c < 8; ++c) va[c] = vcol[c * (kLdsRow / 2) + 32 * mt];
-          const bf16x8 av = __builtin_bit_cast(bf16x8, va);
+          const unsigned char* vm = vb + (mt >> 1) * kBlockBytes;
+          const bf16x4 lo = lds_read_tr4(vm + v_off[mt & 1][0]);
+          const bf16x4 hi = lds_read_tr4(vm + v_off[mt & 1][1]);
+          const bf16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           acc[mt][0] = mfma32(av, bp0, acc[mt][0]);
           acc[mt][1] = mfma32(av, bp1, acc[mt][1]);
         }
@@ -524,6 +628,8 @@ int check_common(const fa_mla_decode_args* a) {
   FA_CHECK_ARG((reinterpret_cast<uintptr_t>(a->kv) & 15) == 0 && (a->kv_block_stride % 16) == 0 &&
                    (a->kv_row_stride % 16) == 0,
                "kv cache rows must be 16-byte aligned");
+  FA_CHECK_ARG(a->kv_row_stride > 0 && a->kv_row_stride <= (1 << 24),
+               "kv_row_stride %lld outside (0, 2^24]", static_cast<long long>(a->kv_row_stride));
   return FA_OK;
 }
 
