@@ -131,6 +131,33 @@ def algorithmic_work(spec, lens_cpu, indices) -> tuple:
     return nbytes, flops
 
 
+def kernel_sources_sha() -> str:
+    """sha256 (16 hex) over the HIP sources and C header, as recorded in profiles/."""
+    import hashlib
+    h = hashlib.sha256()
+    for d in (os.path.join(ROOT, "flagattention_amd", "csrc"), os.path.join(ROOT, "include")):
+        for f in sorted(os.listdir(d)):
+            if f.endswith((".hip", ".h")):
+                h.update(f.encode())
+                with open(os.path.join(d, f), "rb") as fh:
+                    h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def recorded_traffic(workload_name: str):
+    """HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE
+    (copy-calibrated, profiles/traffic.json) -- only if recorded for these exact kernel
+    sources; otherwise None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        rec = json.load(fh).get(workload_name)
+    if not rec or rec.get("csrc_sha") != kernel_sources_sha():
+        return None
+    return int(rec["hbm_read_bytes"]) + int(rec["hbm_write_bytes"])
+
+
 def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
     """The oracle (fp32 PyTorch restatement of the reference's CPU path) on a bounded
     sample of the workload's sequences, scaled to a full step."""
@@ -224,12 +251,15 @@ def main() -> None:
     mfma_frac = tflops / PEAK_BF16_TFLOPS
     # the bound is the roof with the larger required time at peak
     bound = "hbm" if nbytes / PEAK_HBM_GBS >= flops / (PEAK_BF16_TFLOPS * 1e3) else "mfma"
+    traffic = recorded_traffic(spec["name"])
     if bound == "hbm":
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(hbm_frac, 4), "traffic": None}
+                "frac": round(hbm_frac, 4), "traffic": traffic}
     else:
         roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(mfma_frac, 4), "traffic": None}
+                "unit": "TFLOP/s", "frac": round(mfma_frac, 4), "traffic": traffic}
+    if traffic is not None:
+        roof["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)"
     roof.update({"kernel": "mla_decode_kernel", "kernel_us_mean": round(dec_us_mean, 2),
                  "kernel_us_median": round(dec_us_med, 2), "bytes_per_launch": nbytes,
                  "flops_per_launch": flops, "hbm_gbs": round(gbs, 1),

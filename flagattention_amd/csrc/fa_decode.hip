@@ -46,8 +46,9 @@ constexpr int kQSteps = kDqk / 16;           // 36 MFMA k-steps for QK
 
 enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 
+// The two tile buffers are separate LDS objects (see the kernel) so the
+// compiler can prove that reads of one never alias the copy into the other.
 struct __attribute__((aligned(16))) Smem {
-  unsigned char kv[2][kTileBytes];   // double-buffered bf16 tiles (blocked layout)
   unsigned char p[kRows * kPRow];    // P as [head][token] bf16
   float red[2][kRows];               // per token-half row maxima
   float lsum[2][kRows];              // per token-half row sums (epilogue)
@@ -81,6 +82,10 @@ __device__ inline void barrier() {
   wait_lds();
   __builtin_amdgcn_s_barrier();
 }
+
+// Wave index as a scalar (the compiler cannot tell that threadIdx.x / 64 is
+// uniform across a wave; LDS addresses derived from it must be scalars).
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 __device__ inline void copy16_to_lds(const unsigned char* src, unsigned char* lds_block) {
   __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
@@ -118,7 +123,7 @@ __device__ inline void copy_block_buf(__amdgpu_buffer_rsrc_t rs, unsigned char* 
 
 __device__ inline void copy_page_rows(unsigned char* buf, const unsigned char* page,
                                       int valid_bytes, const unsigned int (&voff)[2]) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(page), 0, valid_bytes,
                                         0x00020000);
@@ -142,7 +147,7 @@ __device__ inline void copy_page_rows(unsigned char* buf, const unsigned char* p
 __device__ inline void copy_gather_rows(unsigned char* buf, const int32_t* rows,
                                         const unsigned char* kv, long long block_stride,
                                         long long row_stride) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int lrow = lane >> 3;
 #pragma unroll
   for (int rl = 0; rl < 2; ++rl) {
@@ -226,9 +231,17 @@ __device__ inline void store_fp8_slice(unsigned char* buf, const Fp8Slice& f, in
   *reinterpret_cast<uintx4*>(buf + tile_off(r, 65 + 2 * qd)) = f.rope[1];
 }
 
+template <int V>
+struct IntTag {
+  static constexpr int value = V;
+};
+
 template <int kMode>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_decode_args a,
                                                                  int num_m_blocks, int htiles) {
+  // double-buffered bf16 tiles (blocked layout); tile t lives in buffer t & 1
+  __shared__ __attribute__((aligned(16))) unsigned char kv_buf0[kTileBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char kv_buf1[kTileBytes];
   __shared__ Smem sm;
 
   // XCD-aware work-group -> (part, m-block): work-groups are dealt round-robin
@@ -255,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
   const int head0 = (mb - s * htiles) * kRows;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = wave_id(), lane = tid & 63;
   const int g = lane >> 5, li = lane & 31;
   const int qh = wave & 1, qt = wave >> 1;
   const float scale_log2 = a.softmax_scale * kLog2e;
@@ -369,8 +382,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       if (wave != 0 || t >= ntiles) return -1;
       return srows[(blk_lo + t) * kPage + lane];
     };
-    auto issue = [&](int t) {  // request the data of tile t into LDS buffer t & 1
-      unsigned char* buf = sm.kv[t & 1];
+    auto issue = [&](int t, unsigned char* buf) {  // request tile t (into `buf` if bf16)
       if constexpr (kMode == kDense) {
         // A page id outside the cache (or a block beyond the table) is read
         // as an all-masked page instead of faulting.
@@ -404,11 +416,11 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     } else {
       next_phys = blk_lo < a.max_blocks_per_seq ? sload(bt + blk_lo) : -1;
     }
-    issue(0);
+    issue(0, kv_buf0);
     if constexpr (kMode == kSparseFp8) {
       wait_vmem();
-      store_fp8_slice(sm.kv[0], f8, f8_r, f8_qd);
-      if (ntiles > 1) issue(1);
+      store_fp8_slice(kv_buf0, f8, f8_r, f8_qd);
+      if (ntiles > 1) issue(1, nullptr);
     }
 
     // Online softmax state, log2 units.  mref is the reference max that P and
@@ -424,23 +436,29 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       acc[i][1] = floatx16{};
     }
 
-    for (int it = 0; it < ntiles; ++it) {
-      const unsigned char* kvb = sm.kv[it & 1];
+    // One tile of work; kPar (= it & 1) selects the buffers at compile time.
+    auto tile_step = [&](const int it, auto par) {
+      constexpr int kPar = decltype(par)::value;
+      const unsigned char* kvb = kPar ? kv_buf1 : kv_buf0;
+      unsigned char* next_buf = kPar ? kv_buf0 : kv_buf1;
       wait_vmem();
       barrier();  // tile it resident; everyone done with tile it-1
       if constexpr (kMode == kSparseFp8) {
-        if (it + 1 < ntiles) store_fp8_slice(sm.kv[(it + 1) & 1], f8, f8_r, f8_qd);
+        if (it + 1 < ntiles) store_fp8_slice(next_buf, f8, f8_r, f8_qd);
       }
-      if (it + kAhead < ntiles) issue(it + kAhead);
+      if (it + kAhead < ntiles) issue(it + kAhead, next_buf);
       if constexpr (kMode != kDense) {
         publish_rows(it + kAhead + 1, next_rows);
         next_rows = load_rows(it + kAhead + 2);
       }
 
       // ---- S^T = K Q^T for 32 tokens x 32 heads ----
+      // A operands stream from LDS kPre steps ahead of their MFMA; the
+      // scheduling groups pin that interleave (the scheduler would otherwise
+      // serialise read -> wait -> MFMA to save registers).
       floatx16 sacc = floatx16{};
       {
-        constexpr int kPre = 6;
+        constexpr int kPre = 4;
         bf16x8 af[kPre];
 #pragma unroll
         for (int k = 0; k < kPre; ++k)
@@ -454,6 +472,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
                 *reinterpret_cast<const bf16x8*>(kvb + a_off[kn & 3] + (kn >> 2) * kBlockBytes);
           }
           sacc = mfma32(cur, qf[k], sacc);
+        }
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (k + kPre < kQSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
       }
 
@@ -481,13 +506,16 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       constexpr float kSlack = 8.f;
       const bool up0 = t0 > mref0 + kSlack || (mref0 == ninf && t0 != ninf);
       const bool up1 = t1 > mref1 + kSlack || (mref1 == ninf && t1 != ninf);
+      // accumulators that already hold something need rescaling (an -inf
+      // reference means nothing has been accumulated yet)
+      const bool rs0 = up0 && mref0 != ninf, rs1 = up1 && mref1 != ninf;
       float al0 = 1.f, al1 = 1.f;
       if (up0) {
-        al0 = exp2f(mref0 - t0);
+        al0 = __builtin_amdgcn_exp2f(mref0 - t0);
         mref0 = t0;
       }
       if (up1) {
-        al1 = exp2f(mref1 - t1);
+        al1 = __builtin_amdgcn_exp2f(mref1 - t1);
         mref1 = t1;
       }
       const float mref = qh ? mref1 : mref0;
@@ -499,8 +527,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         unsigned char* prow = sm.p + (32 * qh + li) * kPRow + (32 * qt + 4 * g) * 2;
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
-          float p0 = exp2f(sv[4 * qd + 0] - mu), p1 = exp2f(sv[4 * qd + 1] - mu);
-          float p2 = exp2f(sv[4 * qd + 2] - mu), p3 = exp2f(sv[4 * qd + 3] - mu);
+          float p0 = __builtin_amdgcn_exp2f(sv[4 * qd + 0] - mu);
+          float p1 = __builtin_amdgcn_exp2f(sv[4 * qd + 1] - mu);
+          float p2 = __builtin_amdgcn_exp2f(sv[4 * qd + 2] - mu);
+          float p3 = __builtin_amdgcn_exp2f(sv[4 * qd + 3] - mu);
           psum += (p0 + p1) + (p2 + p3);
           uintx2 w;
           w[0] = pack_bf16x2(p0, p1);
@@ -509,33 +539,73 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         }
         lpart = lpart * (qh ? al1 : al0) + psum;
       }
-      if (__any(up0 || up1)) {  // rare after the first tile
+      if (__any(rs0 || rs1)) {  // rare: only when a running max jumps by > 2^8
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           acc[i][0] *= al0;
+          __builtin_amdgcn_sched_barrier(0);
           acc[i][1] *= al1;
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       barrier();
 
       // ---- O^T[128 dims x 64 heads] += V^T P^T ----
+      // Operands of k-step kk+1 (2 P^T reads, 8 V^T transpose reads) are
+      // issued while the 8 MFMAs of k-step kk run.
+      {
+        bf16x8 bp[2][2];
+        bf16x4 va[2][4][2];
+        auto load_pv = [&](int kk, int slot) {
+          bp[slot][0] =
+              *reinterpret_cast<const bf16x8*>(sm.p + li * kPRow + (16 * kk + 8 * g) * 2);
+          bp[slot][1] =
+              *reinterpret_cast<const bf16x8*>(sm.p + (32 + li) * kPRow + (16 * kk + 8 * g) * 2);
+          const unsigned char* vb = kvb + kk * 2 * kRowGroupBytes;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 bp0 =
-            *reinterpret_cast<const bf16x8*>(sm.p + li * kPRow + (16 * kk + 8 * g) * 2);
-        const bf16x8 bp1 =
-            *reinterpret_cast<const bf16x8*>(sm.p + (32 + li) * kPRow + (16 * kk + 8 * g) * 2);
-        const unsigned char* vb = kvb + kk * 2 * kRowGroupBytes;
+          for (int mt = 0; mt < 4; ++mt) {
+            const unsigned char* vm = vb + (mt >> 1) * kBlockBytes;
+            va[slot][mt][0] = lds_read_tr4(vm + v_off[mt & 1][0]);
+            va[slot][mt][1] = lds_read_tr4(vm + v_off[mt & 1][1]);
+          }
+        };
+        load_pv(0, 0);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const unsigned char* vm = vb + (mt >> 1) * kBlockBytes;
-          const bf16x4 lo = lds_read_tr4(vm + v_off[mt & 1][0]);
-          const bf16x4 hi = lds_read_tr4(vm + v_off[mt & 1][1]);
-          const bf16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[mt][0] = mfma32(av, bp0, acc[mt][0]);
-          acc[mt][1] = mfma32(av, bp1, acc[mt][1]);
+        for (int kk = 0; kk < 4; ++kk) {
+          const int cs = kk & 1;
+          if (kk + 1 < 4) load_pv(kk + 1, cs ^ 1);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            const bf16x8 av =
+                __builtin_shufflevector(va[cs][mt][0], va[cs][mt][1], 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[mt][0] = mfma32(av, bp[cs][0], acc[mt][0]);
+            acc[mt][1] = mfma32(av, bp[cs][1], acc[mt][1]);
+          }
+        }
+        // reads of step 0, then per step: 8 MFMAs interleaved with the
+        // next step's 10 reads
+#pragma unroll
+        for (int i = 0; i < 10; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (kk + 1 < 4) {
+              if (i < 2) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+              } else {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+              }
+            }
+          }
         }
       }
+    };
+
+    for (int it = 0; it < ntiles; it += 2) {
+      tile_step(it, IntTag<0>{});
+      if (it + 1 < ntiles) tile_step(it + 1, IntTag<1>{});
     }
 
     // ---- epilogue: row sums, normalise, write out / partials ----
@@ -555,7 +625,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         bf16* orow = static_cast<bf16*>(a.out) +
                      ((static_cast<long long>(b) * a.s_q + s) * a.h_q + head) * kDv + dim0;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
             uintx2 w;
@@ -563,6 +633,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             w[1] = pack_bf16x2(acc[mt][nt][4 * qd + 2] * inv, acc[mt][nt][4 * qd + 3] * inv);
             *reinterpret_cast<uintx2*>(orow + 32 * mt + 8 * qd) = w;
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
         if (wave == 0 && g == 0)
           a.lse[(static_cast<long long>(b) * a.h_q + head) * a.s_q + s] = lse_v;
       } else if (split_ok) {
@@ -570,7 +642,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             static_cast<long long>(ns0 + split_local) * (a.s_q * a.h_q) + s * a.h_q + head;
         float* orow = a.o_accum + prow * kDv + dim0;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
             floatx4 w;
@@ -580,6 +652,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             w[3] = acc[mt][nt][4 * qd + 3] * inv;
             *reinterpret_cast<floatx4*>(orow + 32 * mt + 8 * qd) = w;
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
         if (wave == 0 && g == 0) a.lse_accum[prow] = lse_v;
       }
     }
