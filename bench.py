@@ -219,11 +219,11 @@ def main() -> None:
     spec = workload_spec(args.workload)
     q, pools, tables, lens, indices = build_inputs(spec, dev, args.copies)
     s_q, h_q, b = spec["s_q"], spec["h_q"], spec["batch"]
-    md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, topk=spec["topk"])
+    md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, num_heads_q=h_q, topk=spec["topk"])
     ws = fa.DecodeWorkspace(b, s_q, h_q, md.shape[0], dev, topk=spec["topk"])
 
     def step(i, events=None):
-        md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, topk=spec["topk"])
+        md, ns = fa.get_mla_metadata(lens, s_q * h_q, 1, num_heads_q=h_q, topk=spec["topk"])
         c = i % len(pools)
         return ws.run(q, pools[c], tables[c], lens, md, ns, SCALE, spec["causal"],
                       spec["fp8"], indices, decode_events=events)

@@ -23,7 +23,7 @@ typedef unsigned int uintx2 __attribute__((ext_vector_type(2)));
 constexpr int kPage = FA_MLA_PAGE_SIZE;   // 64 tokens per page / tile
 constexpr int kDqk = FA_MLA_D_QK;         // 576
 constexpr int kDv = FA_MLA_D_V;           // 512
-constexpr int kRows = FA_MLA_ROWS_PER_TILE;  // 64 query rows per work-group
+constexpr int kRows = FA_MLA_ROWS_PER_TILE;  // 128 query rows per work-group
 constexpr int kMdStride = FA_MLA_MD_STRIDE;
 
 constexpr float kLog2e = 1.4426950408889634f;

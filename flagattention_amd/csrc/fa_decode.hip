@@ -1,52 +1,60 @@
 // MLA decode kernels for gfx950: dense paged, sparse top-k bf16, sparse fp8.
 //
-// One work-group = 8 waves = 64 query rows (heads head0..head0+63 of query
-// token s) x one scheduler part (a run of 64-token KV pages, possibly spanning
-// several sequences).  The part is processed as 32-token tiles (half pages)
-// through a 4-buffer LDS ring.  The waves specialise, one of each kind per
-// SIMD, so the MFMAs of one kind run while the other waits on LDS, barriers
-// or its softmax:
-//   * QK waves (0-3): S^T = K Q^T for tile t+1 on MFMA 16x16x32 bf16; wave
-//     (qh, qt) covers 16 tokens (qt) x 32 heads (qh) and keeps its Q^T operand
-//     (32 heads x 576) in registers for the whole sequence; then the online
-//     softmax (log2 domain; the two token halves' row maxima meet in LDS) and
-//     P (bf16) into LDS;
-//   * PV waves (4-7): request tile t+3 (HBM -> LDS, no VGPR staging, two
-//     steps ahead of its use) and O^T += V^T P^T for tile t on MFMA 32x32x16
-//     bf16; wave w owns value dims [128w, 128w+128) for all 64 heads, its V^T
-//     operands read from the row-major tile with ds_read_b64_tr_b16.
-// Two barriers per tile: one when the tile's data / P / buffers are ready,
-// one for the row-max exchange.  Accumulators are rescaled only when a running
-// max grows by more than 2^8.  Unsplit sequences are normalised and written as
-// bf16 out / fp32 lse; split ones write fp32 (o, lse) partials for
-// fa_mla_combine.
+// One work-group = 4 waves (one per SIMD) = 128 query rows (32 per wave; a
+// row is a (query token, head) pair) x one scheduler part (a run of 64-token
+// KV pages, possibly spanning several sequences).  All 128 rows share one
+// stream of KV tiles, so every tile enters the CU once: the rate at which a
+// CU can take in data, not the HBM, is what bounds this kernel when two
+// work-groups each pull the same tile.
+//
+// The part is processed as 32-token tiles (half pages) through a 4-buffer LDS
+// ring; wave w of the work-group copies row-group w of every tile (HBM -> LDS,
+// no VGPR staging) three tiles ahead.  Each wave owns its 32 rows end to end:
+//   * S^T = K Q^T for its 32 rows on MFMA 32x32x16 bf16 (one lane per row,
+//     16 of the 32 tokens in its registers), its Q^T operand (32 rows x 576)
+//     kept in VGPRs for the whole sequence;
+//   * the online softmax entirely in registers (log2 domain, lazy rescale when
+//     a row max grows by more than 2^8);
+//   * O^T += V^T P^T on MFMA 32x32x16 bf16 for all 512 value dims (the 256
+//     fp32 accumulators of its rows sit in AGPRs).  The S accumulator layout
+//     is exactly the P^T operand layout of the next MFMA when the 16 tokens
+//     of a k-step are taken in the order 8(e/4) + 4(lane/32) + e%4, so P never
+//     leaves the registers; V^T is read in that token order with
+//     ds_read_b64_tr_b16.
+// Step t runs QK(t+1), then PV(t) with the softmax of tile t+1 under it; one
+// barrier per tile (the copied tile is shared by the four waves).
+// Unsplit sequences are normalised and written as bf16 out / fp32 lse; split
+// ones write fp32 (o, lse) partials for fa_mla_combine.
 //
 // LDS tile layout: the 32 x 72 grid of 16-byte chunks (row r, logical chunk
 // k) is stored as 4 row-groups x 9 chunk-groups of 1 KB blocks.  Block
 // (r/8, k/8) holds slot (r%8)*8 + ((k%8) ^ swz(r)), swz(r) = (r&7)^((r>>3)&1).
 // One wave-wide copy fills exactly one block, so every copy lane has a fixed
-// source offset; the XOR keeps the QK operand reads (16 rows x one chunk)
-// free of bank conflicts.
+// source offset; the XOR keeps the QK operand reads and the V^T transpose
+// reads free of bank conflicts.
 //
 // Reference lineage: gather + online softmax of _paged_attn_kernel
 // (src/flag_attn/paged.py:296-337) and the per-split (o, lse) epilogue of
 // _fwd_split_kv_kernel (src/flag_attn/split_kv.py:161-174).
+#include <utility>
+
 #include "fa_common.h"
 
 namespace fa {
 namespace {
 
-constexpr int kThreads = 512;  // 4 QK/softmax waves + 4 PV/copy waves
+constexpr int kThreads = 256;  // 4 waves, one per SIMD
 constexpr int kTileRows = 32;                    // tokens per pipeline tile
 constexpr int kRowBytes = kDqk * 2;              // 1152 B: one bf16 cache row
 constexpr int kChunkGroups = kRowBytes / 128;    // 9 groups of 8 chunks per row
 constexpr int kBlockBytes = 1024;                // 8 rows x 8 chunks
 constexpr int kRowGroupBytes = kChunkGroups * kBlockBytes;  // 9216
 constexpr int kTileBytes = kTileRows * kRowBytes;  // 36864 B per LDS tile
-constexpr int kPRow = kTileRows * 2 + 16;        // 80 B per P row (32 bf16 + pad)
-constexpr int kPBytes = kRows * kPRow;           // 5120
 constexpr int kFp8RowBytes = FA_MLA_FP8_ROW_BYTES;  // 656
-constexpr int kQSteps = kDqk / 32;               // 18 MFMA k-steps for QK
+constexpr int kQSteps = kDqk / 16;               // 36 MFMA k-steps for QK
+constexpr int kWaveRows = 32;                    // query rows per wave
+constexpr int kQRegs = 33;                       // QK k-steps whose Q operand stays in VGPRs
+constexpr int kDimTiles = kDv / 32;              // 16 MFMA row tiles of O^T
 constexpr int kSlots = 8;                        // ring of per-tile metadata slots
 constexpr int kCopiesPerWave = kChunkGroups;     // 9 wave-wide copies per tile
 
@@ -56,13 +64,10 @@ enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 // kernel) so the compiler can prove reads of one never alias a copy into
 // another.
 struct __attribute__((aligned(16))) Smem {
-  unsigned char p[2][kPBytes];       // P of a tile as [head][token] bf16, by tile parity
-  // Per-head tile max (then row sums, in the epilogue) as written by the QK
-  // waves: [token half qt][head half qh][head % 16][(head / 16) % 2], so each
-  // lane stores its two heads with one 8-byte write.
-  float red[2][2][16][2];
-  float lsum[2][2][16][2];
-  unsigned int vmask[kSlots];        // valid-key bitmask of tile u in slot u % kSlots
+  // Q^T operands of the last k-steps, per wave and lane (16 B each)
+  unsigned char qx[4][kQSteps - kQRegs][64 * 16];
+  unsigned int vmask[kSlots];  // valid-key bitmask of tile u in slot u % kSlots
+  unsigned int redo;           // a row of the sequence needs the second pass
 };
 
 // Source of masked gather rows: every lane issues its copy (so each wave has
@@ -81,6 +86,13 @@ __device__ inline int tile_off(int r, int k) {
 __device__ inline floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+// The same MFMA with its accumulator pinned to VGPRs: the 256 AGPRs hold the
+// O accumulators, and an S accumulator placed among them would evict one.
+// Its operands come from LDS / global reads (no VALU-write -> MFMA-read
+// hazard window); its result is read by VALU only after a barrier.
+__device__ inline void mfma32_vacc(bf16x8 a, bf16x8 b, floatx16& c) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
 __device__ inline floatx4 mfma16(bf16x8 a, bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -94,9 +106,14 @@ __device__ inline T sload(const T* p) {
 }
 
 __device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
+// Work-group barrier that also fences the instruction scheduler: the phases
+// between barriers are laid out by hand (which MFMAs run under which other
+// wave's work), so nothing may move across.
 __device__ inline void barrier() {
+  __builtin_amdgcn_sched_barrier(0);
   wait_lds();
   __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 }
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt low bits [3:0], high bits [15:14]).
 template <int N>
@@ -147,22 +164,6 @@ __device__ inline const unsigned char* uniform(const unsigned char* p) {
   const unsigned int lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v));
   const unsigned int hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v >> 32));
   return reinterpret_cast<const unsigned char*>((static_cast<unsigned long long>(hi) << 32) | lo);
-}
-
-__device__ inline void copy_half_page(unsigned char* buf, int rg, const unsigned char* base,
-                                      int valid_bytes, unsigned int voff) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<unsigned char*>(uniform(base)), 0, uniform(valid_bytes), 0x00020000);
-  unsigned char* dst = buf + rg * kRowGroupBytes;
-  copy_block_buf<0>(rs, dst, voff);
-  copy_block_buf<1>(rs, dst, voff);
-  copy_block_buf<2>(rs, dst, voff);
-  copy_block_buf<3>(rs, dst, voff);
-  copy_block_buf<4>(rs, dst, voff);
-  copy_block_buf<5>(rs, dst, voff);
-  copy_block_buf<6>(rs, dst, voff);
-  copy_block_buf<7>(rs, dst, voff);
-  copy_block_buf<8>(rs, dst, voff);
 }
 
 // Gathered rows (sparse bf16): `row` is this lane's source row (a cache row
@@ -225,9 +226,11 @@ __device__ inline floatx2 fp8x2_to_f32(unsigned int word) {
 }
 
 __device__ inline unsigned int pack_bf16x2(float a, float b) {
-  bf16 x = static_cast<bf16>(a), y = static_cast<bf16>(b);
-  return static_cast<unsigned int>(__builtin_bit_cast(unsigned short, x)) |
-         (static_cast<unsigned int>(__builtin_bit_cast(unsigned short, y)) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  floatx2 f;
+  f[0] = a;
+  f[1] = b;
+  return __builtin_bit_cast(unsigned int, __builtin_convertvector(f, bf16x2));  // one v_cvt_pk_bf16_f32
 }
 
 // Raw fp8 row slice held by one thread: (tile row r, eighth p) -> 64 latent
@@ -273,9 +276,20 @@ struct IntTag {
   static constexpr int value = V;
 };
 
+// f(IntTag<0>{}), ..., f(IntTag<N-1>{}): an unrolled loop whose index is a
+// compile-time constant (needed for instruction immediates).
+template <typename F, int... Is>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(IntTag<Is>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int kMode>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_decode_args a,
-                                                                 int num_m_blocks, int htiles) {
+                                                                 int num_m_blocks) {
   // ring of four bf16 tiles (blocked layout); tile u lives in buffer u % 4
   __shared__ __attribute__((aligned(16))) unsigned char kv_buf0[kTileBytes];
   __shared__ __attribute__((aligned(16))) unsigned char kv_buf1[kTileBytes];
@@ -285,8 +299,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #define FA_KVBUF(i) ((i) == 0 ? kv_buf0 : (i) == 1 ? kv_buf1 : (i) == 2 ? kv_buf2 : kv_buf3)
 
   // XCD-aware work-group -> (part, m-block): work-groups are dealt round-robin
-  // over the 8 XCDs, so the m-blocks of one part share an XCD (and its L2)
-  // and read each KV tile from HBM once.
+  // over the 8 XCDs, so the m-blocks of one part share an XCD (and its L2).
   const int wg = blockIdx.x;
   int part, mb;
   if ((a.num_parts & 7) == 0) {
@@ -304,41 +317,69 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
   const int b_end = sload(md + 2), blk_end = sload(md + 3);
   const int first_local = sload(md + 4);
 
-  const int s = mb / htiles;
-  const int head0 = (mb - s * htiles) * kRows;
-
-  // Waves 0-3 compute S = QK^T and the softmax; waves 4-7 request tiles and
-  // compute O += PV.  Waves are spread over the four SIMDs in order, so every
-  // SIMD runs one wave of each kind and the MFMAs of one fill the other's
-  // waits.
   const int tid = threadIdx.x;
-  const int wave = wave_id();
-  const bool qk_role = wave < 4;
-  const int w4 = wave & 3;
-  const int lane = tid & 63;
-  const int g = lane >> 5, li = lane & 31;    // PV lane split (32x32 MFMA)
-  const int g4 = lane >> 4, l16 = lane & 15;  // QK lane split (16x16 MFMA)
-  const int lrow = lane >> 3;                 // copy lanes: row 8*w4 + lrow of a tile
+  const int wave = wave_id(), lane = tid & 63;
+  const int g = lane >> 5, li = lane & 31;
+  const int lrow = lane >> 3;  // copy lanes: row 8*wave + lrow of a tile
+  // This lane's query row (query token s_row, head h_row), 128 rows per
+  // work-group, 32 per wave.  Dense: rows are the flattened (s, h) pairs
+  // (all query tokens see the same keys).  Sparse: one query token per
+  // work-group (each token has its own top-k keys).
+  const int rows_total = a.s_q * a.h_q;
+  int row, s_row, h_row;
+  bool row_ok;
+  if constexpr (kMode == kDense) {
+    row = mb * kRows + wave * kWaveRows + li;
+    row_ok = row < rows_total;
+    s_row = row_ok ? row / a.h_q : 0;
+    h_row = row_ok ? row - s_row * a.h_q : 0;
+  } else {
+    const int htiles = cdiv(a.h_q, kRows);
+    s_row = mb / htiles;
+    const int h = (mb - s_row * htiles) * kRows + wave * kWaveRows + li;
+    row_ok = h < a.h_q;
+    h_row = row_ok ? h : 0;
+    row = s_row * a.h_q + h_row;
+  }
   const float scale_log2 = a.softmax_scale * kLog2e;
   const float ninf = -__builtin_inff();
   const int topk_pad = (a.topk + kPage - 1) / kPage * kPage;
   const long long row_stride = a.kv_row_stride, block_stride = a.kv_block_stride;
-  constexpr float kSlack = 8.f;
 
   const unsigned char* kv = static_cast<const unsigned char*>(a.kv);
   const bf16* q = static_cast<const bf16*>(a.q);
 
-  // Raise a reference max to a tile max when it grows by more than kSlack
-  // (or from -inf); returns the factor that rescales what was accumulated.
-  // mref is the reference that P and the accumulators are relative to (log2
-  // units); most tiles leave it unchanged, so most tiles skip the rescale, and
-  // P stays <= 2^kSlack.
-  auto raise_ref = [&](float& mref, float tmax) -> float {
-    const bool up = (tmax > mref + kSlack) | ((mref == ninf) & (tmax != ninf));
-    const float al = up ? __builtin_amdgcn_exp2f(mref - tmax) : 1.f;
-    mref = up ? tmax : mref;
-    return al;
-  };
+  // ---- per-lane LDS offsets, fixed for the kernel ----
+  // QK A operand (32x32x16): token row li, logical chunk 2k + g of k-step k;
+  // bases by k % 4, k / 4 selects the chunk-group block (+1 KB each).
+  int a_off[4];
+  {
+    const int base = (li >> 3) * kRowGroupBytes + 128 * (li & 7);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a_off[j] = base + 16 * ((2 * j + g) ^ swz(li));
+  }
+  // V^T operand of PV (dims 32mt + li, k-step kk): element e is token
+  // 16kk + 8(e/4) + 4g + e%4, the order in which this lane holds P.  Each
+  // transpose read covers 4 tokens: the 16-lane group (g, half16) reads token
+  // rows 16kk + 8h + 4g + c (c = (lane&15)>>2) at dims 32mt + 16 half16 +
+  // 4 qq (qq = lane&3).  Bases by (mt parity, h); kk adds two row-groups and
+  // mt/2 one chunk-group.
+  int v_off[2][2];
+  {
+    const int half16 = (lane >> 4) & 1, c = (lane & 15) >> 2, qq = lane & 3;
+    const int rr = 4 * g + c;  // token row in its row-group
+#pragma unroll
+    for (int mp = 0; mp < 2; ++mp)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kl = 4 * mp + 2 * half16 + (qq >> 1);  // logical chunk in its group
+        v_off[mp][h] = h * kRowGroupBytes + 16 * (rr * 8 + (kl ^ rr ^ h)) + 8 * (qq & 1);
+      }
+  }
+  // Dense copy lane offset inside a half page: row 8*wave + lrow, chunk
+  // (lane%8) ^ swz(row) of each 128-byte group.
+  const unsigned int page_voff = static_cast<unsigned int>(
+      (8 * wave + lrow) * static_cast<int>(row_stride) + 16 * ((lane & 7) ^ lrow ^ (wave & 1)));
 
   // Metadata from another batch / topk must not drive accesses out of bounds:
   // sequence, block and split indices are clamped to this call's shapes.
@@ -355,292 +396,189 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     const int tok_lo = blk_lo * kPage;
     const int tok_hi = min(blk_hi * kPage, kMode == kDense ? seqlen : a.topk);
     const int ntiles = (tok_hi - tok_lo + kTileRows - 1) / kTileRows;
-    // keys visible to this m-block's query token (dense; bottom-right causal)
-    const int limit = (kMode == kDense && a.causal) ? seqlen - a.s_q + 1 + s : seqlen;
+    const int split_local = (b == b_begin) ? first_local : 0;
+    const int ns0 = sload(a.num_splits + b);
+    const int nsplit = sload(a.num_splits + b + 1) - ns0;
+    const bool split_ok = ns0 >= 0 && split_local >= 0 && ns0 + split_local < max_split;
+    // Keys this row may see (dense, bottom-right causal), relative to the
+    // segment start; tiles from causal_from on need the per-row check.
+    const int row_limit =
+        ((kMode == kDense && a.causal) ? seqlen - a.s_q + 1 + s_row : seqlen) - tok_lo;
+    const int causal_from =
+        (kMode == kDense && a.causal) ? (seqlen - a.s_q + 1 - tok_lo) / kTileRows : ntiles;
+    const int32_t* bt = a.block_table + static_cast<long long>(b) * a.bt_stride_b;
+    const int32_t* srows =
+        kMode == kDense ? nullptr
+                        : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s_row) * topk_pad;
 
-    if (qk_role) {
-      // ======================= S = QK^T and softmax =======================
-      const int qh = w4 & 1, qt = w4 >> 1;
-      // QK A operand: token row 16qt + l16, logical chunk 4k + g4 of k-step k.
-      // Bases by k % 2; k / 2 selects the chunk-group block (+1 KB each).
-      int a_off[2];
-      {
-        const int r = 16 * qt + l16;
-        const int base = (r >> 3) * kRowGroupBytes + 128 * (r & 7);
+    // ---- Q^T operand: dims 16k + 8g .. +7 of this lane's row ----
+    // k < kQRegs in VGPRs (qf), the last k-steps in this wave's LDS slot
+    // (qx): the register file is full (O accumulators + Q + the pipeline).
+    bf16x8 qf[kQRegs];
+    {
+      bf16x8 qrest[kQSteps - kQRegs];
+      if (row_ok) {
+        const bf16* qrow =
+            q + b * a.q_stride_b + s_row * a.q_stride_s + h_row * a.q_stride_h + 8 * g;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) a_off[j] = base + 16 * ((4 * j + g4) ^ swz(r));
+        for (int k = 0; k < kQRegs; ++k) qf[k] = *reinterpret_cast<const bf16x8*>(qrow + 16 * k);
+#pragma unroll
+        for (int k = kQRegs; k < kQSteps; ++k)
+          qrest[k - kQRegs] = *reinterpret_cast<const bf16x8*>(qrow + 16 * k);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kQRegs; ++k) qf[k] = bf16x8{};
+#pragma unroll
+        for (int k = kQRegs; k < kQSteps; ++k) qrest[k - kQRegs] = bf16x8{};
       }
-      auto qk_read = [&](const unsigned char* kb, int k) -> bf16x8 {
-        return *reinterpret_cast<const bf16x8*>(kb + a_off[k & 1] + (k >> 1) * kBlockBytes);
-      };
-      // Q^T operand: qf[nt][k] = head head0 + 32qh + 16nt + l16, dims 32k + 8g4 .. +7
-      bf16x8 qf[2][kQSteps];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int head = head0 + 32 * qh + 16 * nt + l16;
-        if (head < a.h_q) {
-          const bf16* qrow =
-              q + b * a.q_stride_b + s * a.q_stride_s + head * a.q_stride_h + 8 * g4;
-#pragma unroll
-          for (int k = 0; k < kQSteps; ++k)
-            qf[nt][k] = *reinterpret_cast<const bf16x8*>(qrow + 32 * k);
-        } else {
-#pragma unroll
-          for (int k = 0; k < kQSteps; ++k) qf[nt][k] = bf16x8{};
-        }
-      }
-      float mq[2] = {ninf, ninf};   // reference max of heads 32qh + 16nt + l16
-      float lpart[2] = {0.f, 0.f};  // their row sums over this lane's tokens
+      for (int k = kQRegs; k < kQSteps; ++k)
+        *reinterpret_cast<bf16x8*>(sm.qx[wave][k - kQRegs] + 16 * lane) = qrest[k - kQRegs];
+    }
+    auto q_op = [&](int k) -> bf16x8 {
+      return k < kQRegs ? qf[k]
+                        : *reinterpret_cast<const bf16x8*>(sm.qx[wave][k - kQRegs] + 16 * lane);
+    };
 
-      // S^T tile (16 tokens x 32 heads per wave): 36 MFMAs, operands read
-      // kPre k-steps ahead (the scheduling groups keep the interleave).
-      auto qk_tile = [&](const unsigned char* kb, floatx4 (&sacc)[2]) {
-        constexpr int kPre = 6;
-        bf16x8 af[kPre];
+    // ---- tile producers (wave w fills row-group w of every tile) ----
+    // bf16 tiles go HBM -> LDS directly, requested three tiles ahead (two
+    // steps of latency slack).  fp8 tiles are loaded into registers three
+    // tiles ahead and dequantised into LDS two tiles ahead.  Every lane
+    // issues the same loads for every tile (masked rows / pages read zeros),
+    // so the vmcnt waits are constants.
+    // dense: page of the block of the next tile to request, looked up at the
+    // end of the previous step (the scalar load completes at the barrier
+    // that starts the next step)
+    int next_page = -1;
+    auto prefetch_page = [&](int u) {
+      if ((u & 1) == 0) {
+        const int blk = blk_lo + (u >> 1);
+        next_page = (u < ntiles && blk < a.max_blocks_per_seq) ? sload(bt + blk) : -1;
+      }
+    };
+    // dense: buffer resource of tile u's half page (rows past the sequence,
+    // or a page id outside the cache, read as zeros) and its key mask
+    auto dense_prep = [&](int u) -> __amdgpu_buffer_rsrc_t {
+      const int blk = blk_lo + (u >> 1), half = u & 1;
+      const bool ok = u < ntiles && next_page >= 0 && next_page < a.num_kv_blocks;
+      const int start = blk * kPage + kTileRows * half;
+      const int nrows = ok ? max(0, min(seqlen - start, kTileRows)) : 0;
+      const unsigned char* base =
+          kv + (ok ? next_page : 0) * block_stride + kTileRows * half * row_stride;
+      if (tid == 0)
+        sm.vmask[u & (kSlots - 1)] = nrows >= kTileRows ? ~0u : ((1u << nrows) - 1u);
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(uniform(base)), 0,
+                                               uniform(nrows * static_cast<int>(row_stride)),
+                                               0x00020000);
+    };
+    auto dense_issue = [&](int u, unsigned char* buf) {
+      const __amdgpu_buffer_rsrc_t rs = dense_prep(u);
+      unsigned char* dst = buf + wave * kRowGroupBytes;
+      static_for<kChunkGroups>([&](auto gt) {
+        copy_block_buf<decltype(gt)::value>(rs, dst, page_voff);
+      });
+    };
+    // sparse: physical row of this lane's tile row for tile u (-1: masked)
+    auto load_row = [&](int u) -> int32_t {
+      const int uu = u < ntiles ? u : ntiles - 1;
+      const int32_t r = srows[(tok_lo + kTileRows * uu) + 8 * wave + lrow];
+      return u < ntiles ? r : -1;
+    };
+    auto row_ptr = [&](int32_t r) -> const unsigned char* {
+      return r >= 0 ? kv + static_cast<long long>(r >> 6) * block_stride +
+                          static_cast<long long>(r & 63) * row_stride
+                    : static_cast<const unsigned char*>(g_zero_row);
+    };
+    auto publish_mask = [&](int u, int32_t r) {  // wave w owns byte w of tile u's mask
+      const unsigned long long bal = __ballot(r >= 0);
+      unsigned int byte = 0;
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) af[k] = qk_read(kb, k);
-#pragma unroll
-        for (int k = 0; k < kQSteps; ++k) {
-          const bf16x8 cur = af[k % kPre];
-          if (k + kPre < kQSteps) af[k % kPre] = qk_read(kb, k + kPre);
-          sacc[0] = mfma16(cur, qf[0][k], sacc[0]);
-          sacc[1] = mfma16(cur, qf[1][k], sacc[1]);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, kPre, 0);
-#pragma unroll
-        for (int k = 0; k < kQSteps; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          if (k + kPre < kQSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-      };
-      // scale, mask, per-head max over this wave's 16 tokens -> red
-      auto mask_max = [&](unsigned int vm, const floatx4 (&sacc)[2], float (&sv)[2][4]) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool ok = (vm >> (16 * qt + 4 * g4 + r)) & 1u;
-          sv[0][r] = ok ? sacc[0][r] * scale_log2 : ninf;
-          sv[1][r] = ok ? sacc[1][r] * scale_log2 : ninf;
-        }
-        float m[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          m[nt] = fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3]));
-          m[nt] = max_xor32(max_xor16(m[nt]));
-        }
-        floatx2 w;  // one 8-byte store (4 lanes store the same value)
-        w[0] = m[0];
-        w[1] = m[1];
-        *reinterpret_cast<floatx2*>(sm.red[qt][qh][l16]) = w;
-      };
-      // P = exp2(S - mref) of this wave's heads and tokens -> pb as [head][token] bf16
-      auto softmax = [&](const float (&sv)[2][4], unsigned char* pb) {
-        const floatx2 r0 = *reinterpret_cast<const floatx2*>(sm.red[0][qh][l16]);
-        const floatx2 r1 = *reinterpret_cast<const floatx2*>(sm.red[1][qh][l16]);
-        const float tq[2] = {fmaxf(r0[0], r1[0]), fmaxf(r0[1], r1[1])};
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int hrow = 32 * qh + 16 * nt + l16;
-          const float al = raise_ref(mq[nt], tq[nt]);
-          const float mu = mq[nt] == ninf ? 0.f : mq[nt];
-          const float p0 = __builtin_amdgcn_exp2f(sv[nt][0] - mu);
-          const float p1 = __builtin_amdgcn_exp2f(sv[nt][1] - mu);
-          const float p2 = __builtin_amdgcn_exp2f(sv[nt][2] - mu);
-          const float p3 = __builtin_amdgcn_exp2f(sv[nt][3] - mu);
-          lpart[nt] = lpart[nt] * al + ((p0 + p1) + (p2 + p3));
-          uintx2 w;
-          w[0] = pack_bf16x2(p0, p1);
-          w[1] = pack_bf16x2(p2, p3);
-          *reinterpret_cast<uintx2*>(pb + hrow * kPRow + (16 * qt + 4 * g4) * 2) = w;
-        }
-      };
+      for (int j = 0; j < 8; ++j) byte |= static_cast<unsigned int>((bal >> (8 * j)) & 1ull) << j;
+      if (lane == 0)
+        reinterpret_cast<unsigned char*>(sm.vmask)[(u & (kSlots - 1)) * 4 + wave] =
+            static_cast<unsigned char>(byte);
+    };
+    int32_t row_next = -1;  // sparse: row for the next tile to request
+    Fp8Slice f8;
+    const int f8_p = lane & 7;
 
-      // prologue: tile 0
-      barrier();  // P0: tile 0 resident
-      {
-        floatx4 sacc[2] = {floatx4{}, floatx4{}};
-        float sv[2][4];
-        qk_tile(kv_buf0, sacc);
-        mask_max(sm.vmask[0], sacc, sv);
-        barrier();  // P1: tile maxima of tile 0 in red
-        softmax(sv, sm.p[0]);
-      }
-      // step t: S and P of tile t+1 (the PV waves consume tile t meanwhile)
-      auto qk_step = [&](const int t, auto tag) {
-        constexpr int K = decltype(tag)::value;  // t % 4
-        const unsigned char* const b_qk = FA_KVBUF((K + 1) & 3);
-        unsigned char* const p_sm = sm.p[(K + 1) & 1];
-        const int u = t + 1;
-        barrier();  // B0: tile t+1 resident; P((t+1) % 2) free
-        const unsigned int vm = u < ntiles ? sm.vmask[u & (kSlots - 1)] : 0u;
-        floatx4 sacc[2] = {floatx4{}, floatx4{}};
-        float sv[2][4];
-        qk_tile(b_qk, sacc);
-        mask_max(vm, sacc, sv);
-        barrier();  // B1: tile maxima of t+1 in red
-        softmax(sv, p_sm);
-      };
-      // Whole rounds of four steps, then the remainder (the loop back-edge
-      // is only taken after step 3, which keeps the compiler's view of the
-      // buffers the same on every iteration).
-      int t = 0;
-      for (; t + 4 <= ntiles; t += 4) {
-        qk_step(t, IntTag<0>{});
-        qk_step(t + 1, IntTag<1>{});
-        qk_step(t + 2, IntTag<2>{});
-        qk_step(t + 3, IntTag<3>{});
-      }
-      if (t < ntiles) {
-        qk_step(t, IntTag<0>{});
-        if (t + 1 < ntiles) {
-          qk_step(t + 1, IntTag<1>{});
-          if (t + 2 < ntiles) qk_step(t + 2, IntTag<2>{});
-        }
-      }
-      // epilogue: row sums of this wave's heads over its 16 tokens
-      {
-        floatx2 w;
-        w[0] = sum_xor32(sum_xor16(lpart[0]));
-        w[1] = sum_xor32(sum_xor16(lpart[1]));
-        *reinterpret_cast<floatx2*>(sm.lsum[qt][qh][l16]) = w;
-      }
-      barrier();  // E0: row sums in lsum
-      barrier();  // E1: outputs written; LDS reused by the next sequence
-    } else {
-      // ==================== tile requests and O += PV =====================
-      const int split_local = (b == b_begin) ? first_local : 0;
-      const int ns0 = sload(a.num_splits + b);
-      const int nsplit = sload(a.num_splits + b + 1) - ns0;
-      const bool split_ok = ns0 >= 0 && split_local >= 0 && ns0 + split_local < max_split;
-      const int copy_end = min(seqlen, limit);
-      const int32_t* bt = a.block_table + static_cast<long long>(b) * a.bt_stride_b;
-      const int32_t* srows =
-          kMode == kDense ? nullptr
-                          : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s) * topk_pad;
+    // ---- online softmax of this lane's row (log2 units) ----
+    // The reference mref that P and the accumulators are relative to is set
+    // by the first tile with a visible key and then kept: a later score
+    // above it only makes P > 1, harmless while S - mref stays below
+    // kHeadroom (P, the row sum and the accumulators stay far inside the fp32
+    // / bf16 range).  So the accumulators are never rescaled.  If some score
+    // climbs past mref + kHeadroom (scores spread over > 2^64), the sequence
+    // is processed again with mref preset to the row max found.
+    constexpr float kHeadroom = 64.f;
+    float mref, mmax, lsum;
+    bool overflow;
+    floatx16 acc[kDimTiles];
 
-      // PV V^T operand via transpose reads: the 16-lane group (g, half16)
-      // reads token rows 16kk + 8g + 4h + c (c = (lane&15)>>2) at dims
-      // 128w + 32mt + 16 half16 + 4 qq (qq = lane&3).  Bases by (mt parity,
-      // h); kk adds two row-groups and mt/2 one chunk-group.
-      int v_off[2][2];
-      {
-        const int half16 = (lane >> 4) & 1, c = (lane & 15) >> 2, qq = lane & 3;
+    auto qk_read = [&](const unsigned char* kb, int k) -> bf16x8 {
+      return *reinterpret_cast<const bf16x8*>(kb + a_off[k & 3] + (k >> 2) * kBlockBytes);
+    };
+    // V^T operand of PV MFMA j (kk = j / 16, mt = j % 16): two transpose reads
+    auto v_read = [&](const unsigned char* kb, int j) -> bf16x8 {
+      const int kk = j >> 4, mt = j & 15;
+      const unsigned char* p = kb + kk * 2 * kRowGroupBytes + (mt >> 1) * kBlockBytes;
+      const bf16x4 lo = lds_read_tr4(p + v_off[mt & 1][0]);
+      const bf16x4 hi = lds_read_tr4(p + v_off[mt & 1][1]);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    // Softmax of tile u from its S: P^T operands (pk[kk] = the tokens of
+    // k-step kk in this lane's order).
+    auto softmax = [&](int u, unsigned int vm, const floatx16& sacc, bf16x8 (&pk)[2]) {
+      float sv[16];
 #pragma unroll
-        for (int mp = 0; mp < 2; ++mp)
+      for (int r = 0; r < 16; ++r) sv[r] = sacc[r] * scale_log2;
+      if (vm != ~0u || u >= causal_from) {  // partial tile (uniform branch)
+        // token 8(r/4) + 4g + r%4 of the tile: bit c_r = 8(r/4) + r%4 of
+        // vm >> 4g, visible while c_r < row_limit - 32u - 4g
+        const unsigned int vmg = vm >> (4 * g);
+        const int lim = row_limit - kTileRows * u - 4 * g;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int rr = 4 * h + c;                        // token row in its row-group
-            const int kl = 4 * mp + 2 * half16 + (qq >> 1);  // logical chunk in its group
-            v_off[mp][h] = g * kRowGroupBytes + 2 * w4 * kBlockBytes +
-                           16 * (rr * 8 + (kl ^ rr ^ g)) + 8 * (qq & 1);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int c = 8 * (r >> 2) + (r & 3);
+          const bool ok = ((vmg >> c) & 1u) && c < lim;
+          sv[r] = ok ? sv[r] : ninf;
+        }
       }
-      // Dense copy lane offset inside a half page: row 8*w4 + lrow, chunk
-      // (lane%8) ^ swz(row) of each 128-byte group.
-      const unsigned int page_voff = static_cast<unsigned int>(
-          (8 * w4 + lrow) * static_cast<int>(row_stride) + 16 * ((lane & 7) ^ lrow ^ (w4 & 1)));
-
-      // ---- tile producers ----
-      // bf16 tiles go HBM -> LDS directly, requested three tiles ahead of
-      // their PV (two steps of latency slack).  fp8 tiles are loaded into
-      // registers three tiles ahead and dequantised into LDS two tiles ahead.
-      // Every lane issues the same loads for every tile (masked rows / pages
-      // read zeros), so the vmcnt waits are constants.
-      // dense: page of the block of the next tile to request, looked up at
-      // the end of the previous step (the scalar load completes at the
-      // barrier that starts the next step)
-      int next_page = -1;
-      auto prefetch_page = [&](int u) {
-        if ((u & 1) == 0) {
-          const int blk = blk_lo + (u >> 1);
-          next_page = (u < ntiles && blk < a.max_blocks_per_seq) ? sload(bt + blk) : -1;
-        }
-      };
-      auto dense_issue = [&](int u, unsigned char* buf) {
-        const int blk = blk_lo + (u >> 1), half = u & 1;
-        // a page id outside the cache is read as an all-masked page
-        const bool ok = u < ntiles && next_page >= 0 && next_page < a.num_kv_blocks;
-        const int start = blk * kPage + kTileRows * half;
-        const int nrows = ok ? max(0, min(copy_end - start, kTileRows)) : 0;
-        const unsigned char* base =
-            kv + (ok ? next_page : 0) * block_stride + kTileRows * half * row_stride;
-        copy_half_page(buf, w4, base, nrows * static_cast<int>(row_stride), page_voff);
-        if (tid == 256) {
-          const int lim = limit - start;
-          sm.vmask[u & (kSlots - 1)] = !ok || lim <= 0 ? 0u
-                                       : lim >= kTileRows ? ~0u
-                                                          : ((1u << lim) - 1u);
-        }
-      };
-      // sparse: physical row of this lane's tile row for tile u (-1: masked)
-      auto load_row = [&](int u) -> int32_t {
-        const int uu = u < ntiles ? u : ntiles - 1;
-        const int32_t r = srows[(tok_lo + kTileRows * uu) + 8 * w4 + lrow];
-        return u < ntiles ? r : -1;
-      };
-      auto row_ptr = [&](int32_t r) -> const unsigned char* {
-        return r >= 0 ? kv + static_cast<long long>(r >> 6) * block_stride +
-                            static_cast<long long>(r & 63) * row_stride
-                      : static_cast<const unsigned char*>(g_zero_row);
-      };
-      auto publish_mask = [&](int u, int32_t r) {  // wave w4 owns byte w4 of tile u's mask
-        const unsigned long long bal = __ballot(r >= 0);
-        unsigned int byte = 0;
+      float m = sv[0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          byte |= static_cast<unsigned int>((bal >> (8 * j)) & 1ull) << j;
-        if (lane == 0)
-          reinterpret_cast<unsigned char*>(sm.vmask)[(u & (kSlots - 1)) * 4 + w4] =
-              static_cast<unsigned char>(byte);
-      };
-      int32_t row_next = -1;  // sparse: row for the next tile to request
-      Fp8Slice f8;
-      const int f8_p = lane & 7;
-
-      float mp[2] = {ninf, ninf};  // reference max of heads 32nt + li
-      floatx16 acc[4][2];
+      for (int r = 1; r < 16; ++r) m = fmaxf(m, sv[r]);
+      m = max_xor32(m);  // the row's max over the 32 tokens
+      mref = mref == ninf ? m : mref;
+      mmax = fmaxf(mmax, m);
+      overflow = overflow | (m > mref + kHeadroom);
+      const float mu = mref == ninf ? 0.f : mref;
+      float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[i][0] = floatx16{};
-        acc[i][1] = floatx16{};
+      for (int r = 0; r < 16; ++r) {
+        sv[r] = __builtin_amdgcn_exp2f(sv[r] - mu);
+        ps += sv[r];
       }
-      // reference update of heads 32nt + li from the tile maxima in red;
-      // returns whether the accumulators need rescaling
-      auto pv_ref_update = [&](float (&al)[2]) -> bool {
-        bool rs = false;
+      lsum += ps;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const float tmax =
-              fmaxf(sm.red[0][nt][li & 15][li >> 4], sm.red[1][nt][li & 15][li >> 4]);
-          const bool had = mp[nt] != ninf;
-          al[nt] = raise_ref(mp[nt], tmax);
-          rs = rs | (had & (al[nt] != 1.f));
-        }
-        return rs;
-      };
-      // PV operands of k-step kk (16 tokens) of the tile in kb / P in pb, one
-      // read each: i = 0, 1 the P^T halves, i = 2..9 the V^T transpose reads
-      bf16x8 bp[2][2];
-      bf16x4 va[2][4][2];
-      auto pv_load = [&](const unsigned char* kb, const unsigned char* pb, int kk, int slot,
-                         int i) {
-        if (i < 2) {
-          bp[slot][i] =
-              *reinterpret_cast<const bf16x8*>(pb + (32 * i + li) * kPRow + (16 * kk + 8 * g) * 2);
-        } else {
-          const int mt = (i - 2) >> 1, h = (i - 2) & 1;
-          va[slot][mt][h] = lds_read_tr4(kb + kk * 2 * kRowGroupBytes + (mt >> 1) * kBlockBytes +
-                                         v_off[mt & 1][h]);
-        }
-      };
-      // PV MFMA j = (mt, nt) = (j / 2, j % 2) of the operands in `slot`
-      auto pv_mfma = [&](int slot, int j) {
-        const int mt = j >> 1, nt = j & 1;
-        const bf16x8 av =
-            __builtin_shufflevector(va[slot][mt][0], va[slot][mt][1], 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[mt][nt] = mfma32(av, bp[slot][nt], acc[mt][nt]);
-      };
+      for (int kk = 0; kk < 2; ++kk) {
+        uintx4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(sv[8 * kk + 2 * i], sv[8 * kk + 2 * i + 1]);
+        pk[kk] = __builtin_bit_cast(bf16x8, w);
+      }
+    };
 
-      // prologue: tiles 0..2 requested, tile 0 resident
+    if (tid == 0) sm.redo = 0u;
+    float mref_start = ninf;
+    for (int pass = 0;; ++pass) {
+      mref = mref_start;
+      mmax = ninf;
+      lsum = 0.f;
+      overflow = false;
+#pragma unroll
+      for (int i = 0; i < kDimTiles; ++i) acc[i] = floatx16{};
+
+      // ---- prologue: tiles 0..2 requested, tile 0 through QK ----
       if constexpr (kMode == kDense) {
         prefetch_page(0);
         dense_issue(0, kv_buf0);
@@ -651,12 +589,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       } else if constexpr (kMode == kSparseBf16) {
         const int32_t r0 = load_row(0), r1 = load_row(1), r2 = load_row(2);
         wait_vmem<0>();
-        copy_gather_row(kv_buf0, w4, row_ptr(r0));
+        copy_gather_row(kv_buf0, wave, row_ptr(r0));
         publish_mask(0, r0);
-        copy_gather_row(kv_buf1, w4, row_ptr(r1));
+        copy_gather_row(kv_buf1, wave, row_ptr(r1));
         publish_mask(1, r1);
         row_next = load_row(3);
-        copy_gather_row(kv_buf2, w4, row_ptr(r2));
+        copy_gather_row(kv_buf2, wave, row_ptr(r2));
         publish_mask(2, r2);
         wait_vmem<18>();  // whatever order the row load took
       } else {
@@ -666,152 +604,184 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         publish_mask(0, r);
         r = load_row(1);
         wait_vmem<0>();
-        store_fp8_slice(kv_buf0, f8, 8 * w4 + lrow, f8_p);
+        store_fp8_slice(kv_buf0, f8, 8 * wave + lrow, f8_p);
         load_fp8_slice(f8, row_ptr(r), f8_p);
         publish_mask(1, r);
         r = load_row(2);
         wait_vmem<0>();
-        store_fp8_slice(kv_buf1, f8, 8 * w4 + lrow, f8_p);
+        store_fp8_slice(kv_buf1, f8, 8 * wave + lrow, f8_p);
         load_fp8_slice(f8, row_ptr(r), f8_p);
         publish_mask(2, r);
         row_next = load_row(3);
       }
-      barrier();  // P0
-      barrier();  // P1: tile maxima of tile 0 in red
+      barrier();
+      floatx16 scur = floatx16{};  // S^T of the tile the next step turns into P
       {
-        float al[2];
-        (void)pv_ref_update(al);  // nothing accumulated yet
+        bf16x8 af[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) af[k] = qk_read(kv_buf0, k);
+#pragma unroll
+        for (int k = 0; k < kQSteps; ++k) {
+          const bf16x8 cur = af[k & 3];
+          if (k + 4 < kQSteps) af[k & 3] = qk_read(kv_buf0, k + 4);
+          mfma32_vacc(cur, q_op(k), scur);
+        }
       }
 
-      // step t: request tile t+3, O += P(t) V(t)
-      auto pv_step = [&](const int t, auto tag) {
+      // ---- step t: QK(t+1) with softmax(t) under it, then PV(t) ----
+      auto step = [&](const int t, auto tag) {
         constexpr int K = decltype(tag)::value;  // t % 4
         unsigned char* const b_pv = FA_KVBUF(K);
+        unsigned char* const b_qk = FA_KVBUF((K + 1) & 3);
         unsigned char* const b_f8 = FA_KVBUF((K + 2) & 3);
         unsigned char* const b_cp = FA_KVBUF((K + 3) & 3);
-        const unsigned char* const p_pv = sm.p[K & 1];
-        // B0: this wave's copies of tile t+1 landed (tile t+2's may still
-        // be in flight), then everyone's; P(t) written; buffer (t+3) % 4 free
+        // this wave's copies of tile t+1 landed (tile t+2's may still be in
+        // flight), then everyone's; everyone is done with step t-1, which
+        // frees buffer (t+3) % 4
         if constexpr (kMode == kSparseFp8) {
           wait_vmem<0>();
         } else {
           wait_vmem<kCopiesPerWave>();
         }
         barrier();
+        __amdgpu_buffer_rsrc_t rs;               // dense requests
+        const unsigned char* gsrc = g_zero_row;  // sparse bf16 requests
         if constexpr (kMode == kDense) {
-          dense_issue(t + 3, b_cp);
-        } else if constexpr (kMode == kSparseBf16) {
+          rs = dense_prep(t + 3);
+        } else {
+          rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
+        }
+        if constexpr (kMode == kSparseBf16) {
           const int32_t r = row_next;
           row_next = load_row(t + 4);
-          copy_gather_row(b_cp, w4, row_ptr(r));
+          gsrc = row_ptr(r) + 16 * ((lane & 7) ^ lrow ^ (wave & 1));
           publish_mask(t + 3, r);
-        } else {
-          store_fp8_slice(b_f8, f8, 8 * w4 + lrow, f8_p);
+        } else if constexpr (kMode == kSparseFp8) {
+          store_fp8_slice(b_f8, f8, 8 * wave + lrow, f8_p);
           load_fp8_slice(f8, row_ptr(row_next), f8_p);
           publish_mask(t + 3, row_next);
           row_next = load_row(t + 4);
         }
+        const unsigned int vm = sm.vmask[t & (kSlots - 1)];
+        unsigned char* const dst = b_cp + wave * kRowGroupBytes;
         __builtin_amdgcn_sched_barrier(0);
-        // k-step 0 operands, then its 8 MFMAs with k-step 1's reads between
+
+        // QK(t+1): 36 MFMAs, K reads 4 ahead, one tile request every 4
+        // MFMAs, the softmax of tile t (VALU) between them
+        floatx16 snext = floatx16{};
+        bf16x8 pk[2];
+        softmax(t, vm, scur, pk);
+        {
+          bf16x8 af[4];
 #pragma unroll
-        for (int i = 0; i < 10; ++i) pv_load(b_pv, p_pv, 0, 0, i);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pv_mfma(0, j);
-          pv_load(b_pv, p_pv, 1, 1, j + 2);
-          if (j < 2) pv_load(b_pv, p_pv, 1, 1, j);
+          for (int k = 0; k < 4; ++k) af[k] = qk_read(b_qk, k);
+          static_for<kQSteps>([&](auto kt) {
+            constexpr int k = decltype(kt)::value;
+            const bf16x8 cur = af[k & 3];
+            if constexpr (k + 4 < kQSteps) af[k & 3] = qk_read(b_qk, k + 4);
+            mfma32_vacc(cur, q_op(k), snext);
+            if constexpr ((k & 3) == 0 && (k >> 2) < kChunkGroups) {
+              constexpr int G = k >> 2;
+              if constexpr (kMode == kDense) {
+                copy_block_buf<G>(rs, dst, page_voff);
+              } else if constexpr (kMode == kSparseBf16) {
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(gsrc + 128 * G),
+                                                 (FA_LDS void*)(dst + G * kBlockBytes), 16, 0, 0);
+              }
+            }
+          });
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // PV(t): 32 MFMAs, V^T reads kVPre MFMAs ahead
+        constexpr int kVPre = 3;
+        {
+          bf16x8 vq[kVPre];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (j < 2) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          } else {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          }
+          for (int j = 0; j < kVPre; ++j) vq[j] = v_read(b_pv, j);
+          static_for<2 * kDimTiles>([&](auto jt) {
+            constexpr int j = decltype(jt)::value;
+            const bf16x8 av = vq[j % kVPre];
+            if constexpr (j + kVPre < 2 * kDimTiles) vq[j % kVPre] = v_read(b_pv, j + kVPre);
+            acc[j & 15] = mfma32(av, pk[j >> 4], acc[j & 15]);
+          });
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 * kVPre, 0);
+          static_for<2 * kDimTiles>([&](auto jt) {
+            constexpr int j = decltype(jt)::value;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if constexpr (j + kVPre < 2 * kDimTiles)
+              __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          });
         }
-        barrier();  // B1: tile maxima of t+1 in red
-        float al[2];
-        const bool rs = pv_ref_update(al);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pv_mfma(1, j);
-        if (__any(rs)) {  // rare: only when a running max jumps by > 2^8
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[i][0] *= al[0];
-            __builtin_amdgcn_sched_barrier(0);
-            acc[i][1] *= al[1];
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        }
+        scur = snext;
         if constexpr (kMode == kDense) prefetch_page(t + 4);
       };
+      // Whole rounds of four steps, then the remainder (the loop back-edge
+      // is only taken after step 3, which keeps the compiler's view of the
+      // buffers the same on every iteration).
       int t = 0;
       for (; t + 4 <= ntiles; t += 4) {
-        pv_step(t, IntTag<0>{});
-        pv_step(t + 1, IntTag<1>{});
-        pv_step(t + 2, IntTag<2>{});
-        pv_step(t + 3, IntTag<3>{});
+        step(t, IntTag<0>{});
+        step(t + 1, IntTag<1>{});
+        step(t + 2, IntTag<2>{});
+        step(t + 3, IntTag<3>{});
       }
       if (t < ntiles) {
-        pv_step(t, IntTag<0>{});
+        step(t, IntTag<0>{});
         if (t + 1 < ntiles) {
-          pv_step(t + 1, IntTag<1>{});
-          if (t + 2 < ntiles) pv_step(t + 2, IntTag<2>{});
+          step(t + 1, IntTag<1>{});
+          if (t + 2 < ntiles) step(t + 2, IntTag<2>{});
         }
       }
       wait_vmem<0>();  // requests for tiles past the end land before LDS is reused
-      barrier();       // E0: row sums in lsum
-
-      // ---- normalise, write out / partials ----
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int head = head0 + 32 * nt + li;
-        if (head >= a.h_q) continue;
-        const float l = sm.lsum[0][nt][li & 15][li >> 4] + sm.lsum[1][nt][li & 15][li >> 4];
-        const float m = mp[nt];
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        const float lse_v = l > 0.f ? (m + log2f(l)) * kLn2 : ninf;
-        const int dim0 = 128 * w4 + 4 * g;
-        if (nsplit == 1) {
-          bf16* orow = static_cast<bf16*>(a.out) +
-                       ((static_cast<long long>(b) * a.s_q + s) * a.h_q + head) * kDv + dim0;
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-              uintx2 w;
-              w[0] = pack_bf16x2(acc[mt][nt][4 * qd + 0] * inv, acc[mt][nt][4 * qd + 1] * inv);
-              w[1] = pack_bf16x2(acc[mt][nt][4 * qd + 2] * inv, acc[mt][nt][4 * qd + 3] * inv);
-              *reinterpret_cast<uintx2*>(orow + 32 * mt + 8 * qd) = w;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          if (w4 == 0 && g == 0)
-            a.lse[(static_cast<long long>(b) * a.h_q + head) * a.s_q + s] = lse_v;
-        } else if (split_ok) {
-          const long long prow =
-              static_cast<long long>(ns0 + split_local) * (a.s_q * a.h_q) + s * a.h_q + head;
-          float* orow = a.o_accum + prow * kDv + dim0;
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-              floatx4 w;
-              w[0] = acc[mt][nt][4 * qd + 0] * inv;
-              w[1] = acc[mt][nt][4 * qd + 1] * inv;
-              w[2] = acc[mt][nt][4 * qd + 2] * inv;
-              w[3] = acc[mt][nt][4 * qd + 3] * inv;
-              *reinterpret_cast<floatx4*>(orow + 32 * mt + 8 * qd) = w;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          if (w4 == 0 && g == 0) a.lse_accum[prow] = lse_v;
-        }
-      }
-      barrier();  // E1
+      if (pass > 0) break;
+      if (__any(overflow) && lane == 0) sm.redo = 1u;
+      barrier();
+      if (sm.redo == 0u) break;
+      mref_start = mmax;  // second pass (rare): the row max is known
     }
+
+    // ---- epilogue: normalise, write out / partials ----
+    const float l = sum_xor32(lsum);
+    if (row_ok) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float lse_v = l > 0.f ? (mref + log2f(l)) * kLn2 : ninf;
+      const int dim0 = 4 * g;  // + 32 mt + 8 qd (+0..3): acc[mt][4qd + i]
+      if (nsplit == 1) {
+        bf16* orow = static_cast<bf16*>(a.out) +
+                     ((static_cast<long long>(b) * a.s_q + s_row) * a.h_q + h_row) * kDv + dim0;
+#pragma unroll
+        for (int mt = 0; mt < kDimTiles; ++mt) {
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            uintx2 w;
+            w[0] = pack_bf16x2(acc[mt][4 * qd + 0] * inv, acc[mt][4 * qd + 1] * inv);
+            w[1] = pack_bf16x2(acc[mt][4 * qd + 2] * inv, acc[mt][4 * qd + 3] * inv);
+            *reinterpret_cast<uintx2*>(orow + 32 * mt + 8 * qd) = w;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (g == 0) a.lse[(static_cast<long long>(b) * a.h_q + h_row) * a.s_q + s_row] = lse_v;
+      } else if (split_ok) {
+        const long long prow = static_cast<long long>(ns0 + split_local) * rows_total + row;
+        float* orow = a.o_accum + prow * kDv + dim0;
+#pragma unroll
+        for (int mt = 0; mt < kDimTiles; ++mt) {
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            floatx4 w;
+            w[0] = acc[mt][4 * qd + 0] * inv;
+            w[1] = acc[mt][4 * qd + 1] * inv;
+            w[2] = acc[mt][4 * qd + 2] * inv;
+            w[3] = acc[mt][4 * qd + 3] * inv;
+            *reinterpret_cast<floatx4*>(orow + 32 * mt + 8 * qd) = w;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (g == 0) a.lse_accum[prow] = lse_v;
+      }
+    }
+    barrier();  // LDS (tiles, masks) is reused by the next sequence
   }
 #undef FA_KVBUF
 }
@@ -864,11 +834,12 @@ int check_common(const fa_mla_decode_args* a) {
 
 template <int kMode>
 int launch_decode(const fa_mla_decode_args* a, hipStream_t stream) {
-  const int htiles = cdiv(a->h_q, kRows);
-  const int num_m_blocks = a->s_q * htiles;
+  // dense: flattened (s, h) rows; sparse: one query token per work-group
+  const int num_m_blocks = kMode == kDense ? cdiv(a->s_q * a->h_q, kRows)
+                                           : a->s_q * cdiv(a->h_q, kRows);
   const int grid = a->num_parts * num_m_blocks;
   hipLaunchKernelGGL(mla_decode_kernel<kMode>, dim3(grid), dim3(kThreads), 0, stream, *a,
-                     num_m_blocks, htiles);
+                     num_m_blocks);
   FA_CHECK_HIP(hipGetLastError());
   return FA_OK;
 }

@@ -35,7 +35,7 @@ from . import _lib
 PAGE_SIZE = 64
 D_QK = 576
 D_V = 512
-ROWS_PER_TILE = 64
+ROWS_PER_TILE = 128
 MD_STRIDE = 8
 FP8_ROW_BYTES = 656
 MAX_BATCH = 4096
@@ -73,14 +73,25 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def num_m_blocks(num_q_tokens_per_head_k: int) -> int:
-    """Work-groups per KV head per part: query rows in tiles of 64."""
+def num_m_blocks(num_q_tokens_per_head_k: int, num_heads_q: Optional[int] = None,
+                 sparse: bool = False) -> int:
+    """Work-groups per KV head per part (query rows in tiles of 128).
+
+    Dense decode tiles the flattened (token, head) rows; sparse decode gives every
+    query token its own tiles (each token has its own key set), which needs
+    ``num_heads_q`` to split the rows into tokens.
+    """
+    if sparse and num_heads_q:
+        s_q = max(1, num_q_tokens_per_head_k // num_heads_q)
+        return s_q * -(-num_heads_q // ROWS_PER_TILE)
     return -(-num_q_tokens_per_head_k // ROWS_PER_TILE)
 
 
-def default_num_parts(cu_count: int, num_q_tokens_per_head_k: int, num_heads_k: int) -> int:
+def default_num_parts(cu_count: int, num_q_tokens_per_head_k: int, num_heads_k: int,
+                      num_heads_q: Optional[int] = None, sparse: bool = False) -> int:
     """One work-group per CU: parts = CUs / (KV heads x row tiles)."""
-    parts = cu_count // (num_heads_k * num_m_blocks(num_q_tokens_per_head_k))
+    parts = cu_count // (num_heads_k * num_m_blocks(num_q_tokens_per_head_k, num_heads_q,
+                                                    sparse))
     return max(1, min(MAX_PARTS, parts))
 
 
@@ -115,7 +126,7 @@ def get_mla_metadata(
     device = cache_seqlens.device
     if num_sm_parts is None:
         num_sm_parts = default_num_parts(device_cu_count(device), num_q_tokens_per_head_k,
-                                         num_heads_k)
+                                         num_heads_k, num_heads_q, topk is not None)
     _require(1 <= num_sm_parts <= MAX_PARTS, f"num_sm_parts outside [1, {MAX_PARTS}]")
     tile_md = torch.empty((num_sm_parts, MD_STRIDE), dtype=torch.int32, device=device)
     num_splits = torch.empty((batch + 1,), dtype=torch.int32, device=device)

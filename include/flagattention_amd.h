@@ -35,7 +35,7 @@ extern "C" {
 #define FA_MLA_PAGE_SIZE 64  /* tokens per KV page (block_size)          */
 #define FA_MLA_D_QK 576      /* 512 latent + 64 rope                     */
 #define FA_MLA_D_V 512       /* value = first 512 latent dims            */
-#define FA_MLA_ROWS_PER_TILE 64  /* query rows (heads) per work-group    */
+#define FA_MLA_ROWS_PER_TILE 128 /* query rows (token, head) per work-group */
 #define FA_MLA_MD_STRIDE 8   /* int32 words per tile-scheduler entry     */
 #define FA_MLA_FP8_ROW_BYTES 656 /* 512 e4m3 + 4 fp32 scales + 64 bf16   */
 #define FA_MLA_MAX_BATCH 4096

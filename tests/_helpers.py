@@ -33,7 +33,7 @@ def run_dense(q, kc, bt, lens, scale, causal=False, parts=None):
 def run_sparse(q, kc, bt, lens, idx, scale, fp8=False, parts=None):
     qd, kd, btd, ld, idd = (t.to(DEV) for t in (q, kc, bt, lens, idx))
     s_q, h_q, topk = q.shape[1], q.shape[2], idx.shape[2]
-    md, ns = fa.get_mla_metadata(ld, s_q * h_q, 1, topk=topk, num_sm_parts=parts)
+    md, ns = fa.get_mla_metadata(ld, s_q * h_q, 1, num_heads_q=h_q, topk=topk, num_sm_parts=parts)
     out, lse = fa.flash_mla_with_kvcache(qd, kd, btd, ld, 512, md, ns, scale, False,
                                          is_fp8_kvcache=fp8, indices=idd)
     torch.cuda.synchronize()

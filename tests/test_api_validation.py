@@ -82,7 +82,9 @@ def test_metadata_rejects(kw, msg):
 
 def test_parts_derivation():
     from flagattention_amd.mla import default_num_parts, num_m_blocks
-    assert num_m_blocks(128) == 2 and num_m_blocks(16) == 1 and num_m_blocks(256) == 4
-    assert default_num_parts(256, 128, 1) == 128
-    assert default_num_parts(256, 256, 1) == 64
+    assert num_m_blocks(128) == 1 and num_m_blocks(16) == 1 and num_m_blocks(256) == 2
+    assert num_m_blocks(256, 128, sparse=True) == 2 and num_m_blocks(200, 100, sparse=True) == 2
+    assert num_m_blocks(200, 100) == 2 and num_m_blocks(32, 16, sparse=True) == 2
+    assert default_num_parts(256, 128, 1) == 256
+    assert default_num_parts(256, 256, 1) == 128
     assert default_num_parts(4, 1024, 1) == 1
