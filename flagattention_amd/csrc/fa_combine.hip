@@ -8,7 +8,9 @@
 // lse = -inf, the convention of src/flag_attn/split_kv.py:161-164.
 //
 // One 64-lane wave per (sequence, query row); each lane owns 8 of the 512
-// value dims, so the fp32 partial rows are read as two 16-byte loads per lane.
+// value dims, so a bf16 partial row is one 16-byte load per lane (partials
+// are stored in bf16: the combine and the decode epilogue move half the
+// bytes, and the weighted sum is accumulated in fp32).
 #include "fa_common.h"
 
 namespace fa {
@@ -18,7 +20,7 @@ constexpr int kCombineThreads = 256;
 constexpr int kRowsPerBlock = kCombineThreads / 64;
 
 __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
-    const float* __restrict__ o_accum, const float* __restrict__ lse_accum,
+    const bf16* __restrict__ o_accum, const float* __restrict__ lse_accum,
     const int32_t* __restrict__ num_splits, bf16* __restrict__ out, float* __restrict__ lse,
     int s_q, int h_q, int max_split) {
   const int rows = s_q * h_q;
@@ -52,13 +54,9 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
     for (int i = 0; i < ns; ++i) {
       const long long r = static_cast<long long>(s0 + i) * rows + row;
       const float w = expf(lse_accum[r] - total);
-      const floatx4* op = reinterpret_cast<const floatx4*>(o_accum + r * kDv + lane * 8);
-      floatx4 a = op[0], c = op[1];
+      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(o_accum + r * kDv + lane * 8);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[j] += w * a[j];
-        acc[4 + j] += w * c[j];
-      }
+      for (int j = 0; j < 8; ++j) acc[j] += w * static_cast<float>(ov[j]);
     }
   }
   bf16x8 v;
@@ -79,7 +77,8 @@ extern "C" int fa_mla_combine(const fa_mla_decode_args* a, void* stream) {
   const int rows = a->s_q * a->h_q;
   dim3 grid(fa::cdiv(rows, fa::kRowsPerBlock), a->batch);
   hipLaunchKernelGGL(fa::mla_combine_kernel, grid, dim3(fa::kCombineThreads), 0,
-                     static_cast<hipStream_t>(stream), a->o_accum, a->lse_accum, a->num_splits,
+                     static_cast<hipStream_t>(stream), static_cast<const fa::bf16*>(a->o_accum),
+                     a->lse_accum, a->num_splits,
                      static_cast<fa::bf16*>(a->out), a->lse, a->s_q, a->h_q,
                      a->batch + a->num_parts);
   FA_CHECK_HIP(hipGetLastError());

@@ -1,28 +1,34 @@
 // MLA decode kernels for gfx950: dense paged, sparse top-k bf16, sparse fp8.
 //
-// One work-group = 4 waves (one per SIMD) = 128 query rows (32 per wave; a
-// row is a (query token, head) pair) x one scheduler part (a run of 64-token
-// KV pages, possibly spanning several sequences).  All 128 rows share one
-// stream of KV tiles, so every tile enters the CU once: the rate at which a
-// CU can take in data, not the HBM, is what bounds this kernel when two
-// work-groups each pull the same tile.
+// One work-group = 4 waves (one per SIMD) = 128 query rows (a row is a
+// (query token, head) pair) x one scheduler part (a run of 64-token KV pages,
+// possibly spanning several sequences).  All 128 rows share one stream of KV
+// tiles, so every tile enters the CU once.
 //
-// The part is processed as 32-token tiles (half pages) through a 4-buffer LDS
-// ring; wave w of the work-group copies row-group w of every tile (HBM -> LDS,
-// no VGPR staging) three tiles ahead.  Each wave owns its 32 rows end to end:
-//   * S^T = K Q^T for its 32 rows on MFMA 32x32x16 bf16 (one lane per row,
-//     16 of the 32 tokens in its registers), its Q^T operand (32 rows x 576)
-//     kept in VGPRs for the whole sequence;
-//   * the online softmax entirely in registers (log2 domain, lazy rescale when
-//     a row max grows by more than 2^8);
-//   * O^T += V^T P^T on MFMA 32x32x16 bf16 for all 512 value dims (the 256
-//     fp32 accumulators of its rows sit in AGPRs).  The S accumulator layout
-//     is exactly the P^T operand layout of the next MFMA when the 16 tokens
-//     of a k-step are taken in the order 8(e/4) + 4(lane/32) + e%4, so P never
-//     leaves the registers; V^T is read in that token order with
-//     ds_read_b64_tr_b16.
-// Step t runs QK(t+1), then PV(t) with the softmax of tile t+1 under it; one
-// barrier per tile (the copied tile is shared by the four waves).
+// The part is processed as 32-token tiles through a 4-buffer LDS ring: tile
+// t+3 is requested (HBM -> LDS, no VGPR staging) when the computation of tile
+// t starts, so three tiles are in flight per CU.  Each tile goes through two
+// phases separated by work-group barriers:
+//   1. S = Q K^T and the softmax, split by rows: wave w owns rows 32w..32w+31
+//      (its Q^T operand, 32 rows x 576 dims, stays in VGPRs), computes their
+//      S on MFMA 16x16x32 bf16 in four independent accumulator chains and
+//      writes P (bf16, against a fixed per-row reference, below) to LDS;
+//   2. O^T += V^T P^T on MFMA 16x16x32 bf16, split by value dims: wave w owns
+//      dims 128w..128w+127 of all 128 rows (256 fp32 accumulators per lane,
+//      in AGPRs).  V^T comes from the tile with transposing LDS reads
+//      (ds_read_b64_tr_b16), P^T from LDS.
+// Splitting PV by dims rather than rows means each wave transposes only its
+// quarter of V: the transposing reads run at about half the rate of plain
+// 16-byte LDS reads, and with a row split every wave would read all of V.
+//
+// Softmax reference: P and the accumulators are relative to a per-row
+// reference mref, set by the first tile in which the row sees a key and then
+// kept.  A later score above it only makes P > 1, harmless while S - mref
+// stays below kHeadroom (P, the row sum and the accumulators stay far inside
+// the fp32 / bf16 range), so the accumulators are never rescaled.  If some
+// score climbs past mref + kHeadroom (scores spread over > 2^64), the
+// sequence is processed again with mref preset to the row max found.
+//
 // Unsplit sequences are normalised and written as bf16 out / fp32 lse; split
 // ones write fp32 (o, lse) partials for fa_mla_combine.
 //
@@ -30,8 +36,8 @@
 // k) is stored as 4 row-groups x 9 chunk-groups of 1 KB blocks.  Block
 // (r/8, k/8) holds slot (r%8)*8 + ((k%8) ^ swz(r)), swz(r) = (r&7)^((r>>3)&1).
 // One wave-wide copy fills exactly one block, so every copy lane has a fixed
-// source offset; the XOR keeps the QK operand reads and the V^T transpose
-// reads free of bank conflicts.
+// source offset; the XOR spreads the K operand reads and the V^T transpose
+// reads over the LDS banks.
 //
 // Reference lineage: gather + online softmax of _paged_attn_kernel
 // (src/flag_attn/paged.py:296-337) and the per-split (o, lse) epilogue of
@@ -43,7 +49,7 @@
 namespace fa {
 namespace {
 
-constexpr int kThreads = 256;  // 4 waves, one per SIMD
+constexpr int kThreads = 256;                    // 4 waves, one per SIMD
 constexpr int kTileRows = 32;                    // tokens per pipeline tile
 constexpr int kRowBytes = kDqk * 2;              // 1152 B: one bf16 cache row
 constexpr int kChunkGroups = kRowBytes / 128;    // 9 groups of 8 chunks per row
@@ -51,23 +57,25 @@ constexpr int kBlockBytes = 1024;                // 8 rows x 8 chunks
 constexpr int kRowGroupBytes = kChunkGroups * kBlockBytes;  // 9216
 constexpr int kTileBytes = kTileRows * kRowBytes;  // 36864 B per LDS tile
 constexpr int kFp8RowBytes = FA_MLA_FP8_ROW_BYTES;  // 656
-constexpr int kQSteps = kDqk / 16;               // 36 MFMA k-steps for QK
-constexpr int kWaveRows = 32;                    // query rows per wave
-constexpr int kQRegs = 33;                       // QK k-steps whose Q operand stays in VGPRs
-constexpr int kDimTiles = kDv / 32;              // 16 MFMA row tiles of O^T
-constexpr int kSlots = 8;                        // ring of per-tile metadata slots
+constexpr int kQkSteps = kDqk / 32;              // 18 MFMA k-steps of QK
+constexpr int kDimTiles = kDv / 4 / 16;          // 8 16-dim tiles of O^T per wave
+constexpr int kRowTiles = kRows / 16;            // 8 16-row tiles
 constexpr int kCopiesPerWave = kChunkGroups;     // 9 wave-wide copies per tile
+constexpr int kQOps = 2 * kQkSteps;              // 36 Q^T operands (k-step, row tile) per wave
+constexpr int kQLds = 11;                         // the last ones live in LDS, not VGPRs
 
 enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 
-// Small shared state; the four tile buffers are separate LDS objects (see the
-// kernel) so the compiler can prove reads of one never alias a copy into
-// another.
+// Shared state beside the three tile buffers (separate LDS objects, see the
+// kernel, so the compiler can prove that reads of one never alias a copy
+// into another).
 struct __attribute__((aligned(16))) Smem {
-  // Q^T operands of the last k-steps, per wave and lane (16 B each)
-  unsigned char qx[4][kQSteps - kQRegs][64 * 16];
-  unsigned int vmask[kSlots];  // valid-key bitmask of tile u in slot u % kSlots
-  unsigned int redo;           // a row of the sequence needs the second pass
+  // P (bf16), row-major [128 rows][32 tokens]; 16-byte chunk c of row r sits
+  // at chunk position c ^ ((r >> 2) & 3).  Between a pass's last PV and the
+  // next P it holds the per-wave second-pass flags, then the row sums.
+  unsigned char p[kRows * 64];
+  // Q^T operands that do not fit in VGPRs: [wave][operand][lane]
+  bf16x8 qx[4][kQLds][64];
 };
 
 // Source of masked gather rows: every lane issues its copy (so each wave has
@@ -83,18 +91,42 @@ __device__ inline int tile_off(int r, int k) {
          16 * (((r & 7) << 3) + ((k & 7) ^ swz(r)));
 }
 
-__device__ inline floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-// The same MFMA with its accumulator pinned to VGPRs: the 256 AGPRs hold the
-// O accumulators, and an S accumulator placed among them would evict one.
-// Its operands come from LDS / global reads (no VALU-write -> MFMA-read
-// hazard window); its result is read by VALU only after a barrier.
-__device__ inline void mfma32_vacc(bf16x8 a, bf16x8 b, floatx16& c) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-}
 __device__ inline floatx4 mfma16(bf16x8 a, bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// The same MFMA with its accumulator kept in VGPRs, for S: the AGPRs hold the
+// O accumulators, and an S accumulator placed among them would evict some.
+// The compiler does not see these MFMAs, so it inserts none of the wait
+// states an MFMA result needs before other instructions read it: every
+// reader of the accumulators goes through mfma_vacc_drain() first.
+__device__ inline void mfma16_vacc(bf16x8 a, bf16x8 b, floatx4& c) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+// First MFMA of a chain (C = 0).  The destination must not overlap A or B (a
+// multi-pass MFMA still reads its sources while it writes), hence the early
+// clobber.
+__device__ inline void mfma16_vacc_first(bf16x8 a, bf16x8 b, floatx4& c) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+// O accumulator MFMA, accumulator tied in AGPRs (the compiler's own form of
+// this MFMA does not keep the accumulator in place, and the copies it then
+// makes between AGPRs cost more than the MFMAs).  Its result is read only in
+// the epilogue, behind mfma_drain().
+__device__ inline void mfma16_aacc(bf16x8 a, bf16x8 b, floatx4& c) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// Wait states after the last inline-asm MFMA before anything reads its
+// result; the scheduling fences keep every instruction on its side.
+__device__ inline void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n s_nop 7");
+  __builtin_amdgcn_sched_barrier(0);
+}
+// 16 wait states (more than an 8-pass MFMA result needs), taking the
+// accumulators as operands so that no read of them is scheduled above it.
+__device__ inline void mfma_vacc_drain(floatx4 (&s)[2][2]) {
+  asm volatile("s_nop 7\n s_nop 7"
+               : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]));
 }
 
 // Load through the scalar unit (constant address space): for wave-uniform
@@ -107,8 +139,7 @@ __device__ inline T sload(const T* p) {
 
 __device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
 // Work-group barrier that also fences the instruction scheduler: the phases
-// between barriers are laid out by hand (which MFMAs run under which other
-// wave's work), so nothing may move across.
+// between barriers are laid out by hand, so nothing may move across.
 __device__ inline void barrier() {
   __builtin_amdgcn_sched_barrier(0);
   wait_lds();
@@ -138,8 +169,8 @@ __device__ inline bf16x4 lds_read_tr4(const unsigned char* p) {
 
 // --- tile copies (row-group rg: tile rows 8rg..8rg+7) ----------------------
 //
-// Lane i of block (w, G) moves row 8w + i/8, logical chunk 8G + ((i%8) ^
-// swz(8w + i/8)).
+// Lane i of block (rg, G) moves row 8rg + i/8, logical chunk 8G + ((i%8) ^
+// swz(8rg + i/8)).
 //
 // Dense half pages use buffer loads: the half page is a scalar buffer
 // resource whose size is its valid bytes, so each copy is one 32-bit lane
@@ -164,19 +195,6 @@ __device__ inline const unsigned char* uniform(const unsigned char* p) {
   const unsigned int lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v));
   const unsigned int hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v >> 32));
   return reinterpret_cast<const unsigned char*>((static_cast<unsigned long long>(hi) << 32) | lo);
-}
-
-// Gathered rows (sparse bf16): `row` is this lane's source row (a cache row
-// or g_zero_row); lane i covers row i/8 of row-group rg.
-__device__ inline void copy_gather_row(unsigned char* buf, int rg, const unsigned char* row) {
-  const int lane = threadIdx.x & 63;
-  const int lrow = lane >> 3;
-  unsigned char* dst = buf + rg * kRowGroupBytes;
-  const unsigned char* src = row + 16 * ((lane & 7) ^ lrow ^ (rg & 1));
-#pragma unroll
-  for (int G = 0; G < kChunkGroups; ++G)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + 128 * G),
-                                     (FA_LDS void*)(dst + G * kBlockBytes), 16, 0, 0);
 }
 
 // Max / sum with the lane 16 (32) positions away: gfx950 lane-swap VALU ops
@@ -290,13 +308,12 @@ __device__ inline void static_for(F&& f) {
 template <int kMode>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_decode_args a,
                                                                  int num_m_blocks) {
-  // ring of four bf16 tiles (blocked layout); tile u lives in buffer u % 4
+  // ring of three bf16 tiles (blocked layout); tile u lives in buffer u % 3
   __shared__ __attribute__((aligned(16))) unsigned char kv_buf0[kTileBytes];
   __shared__ __attribute__((aligned(16))) unsigned char kv_buf1[kTileBytes];
   __shared__ __attribute__((aligned(16))) unsigned char kv_buf2[kTileBytes];
-  __shared__ __attribute__((aligned(16))) unsigned char kv_buf3[kTileBytes];
   __shared__ Smem sm;
-#define FA_KVBUF(i) ((i) == 0 ? kv_buf0 : (i) == 1 ? kv_buf1 : (i) == 2 ? kv_buf2 : kv_buf3)
+#define FA_KVBUF(i) ((i) == 0 ? kv_buf0 : (i) == 1 ? kv_buf1 : kv_buf2)
 
   // XCD-aware work-group -> (part, m-block): work-groups are dealt round-robin
   // over the 8 XCDs, so the m-blocks of one part share an XCD (and its L2).
@@ -319,28 +336,41 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 
   const int tid = threadIdx.x;
   const int wave = wave_id(), lane = tid & 63;
-  const int g = lane >> 5, li = lane & 31;
-  const int lrow = lane >> 3;  // copy lanes: row 8*wave + lrow of a tile
-  // This lane's query row (query token s_row, head h_row), 128 rows per
-  // work-group, 32 per wave.  Dense: rows are the flattened (s, h) pairs
-  // (all query tokens see the same keys).  Sparse: one query token per
-  // work-group (each token has its own top-k keys).
+  const int G = lane >> 4, i16 = lane & 15;
+  const int lrow = lane >> 3;  // copy lanes: tile row 8*wave + lrow
+
+  // Query rows of the work-group.  Dense: the flattened (s, h) pairs mb*128..
+  // (all query tokens see the same keys).  Sparse: heads hbase.. of one query
+  // token (each token has its own top-k keys).
   const int rows_total = a.s_q * a.h_q;
-  int row, s_row, h_row;
-  bool row_ok;
-  if constexpr (kMode == kDense) {
-    row = mb * kRows + wave * kWaveRows + li;
-    row_ok = row < rows_total;
-    s_row = row_ok ? row / a.h_q : 0;
-    h_row = row_ok ? row - s_row * a.h_q : 0;
-  } else {
+  int s_fix = 0, hbase = 0;
+  if constexpr (kMode != kDense) {
     const int htiles = cdiv(a.h_q, kRows);
-    s_row = mb / htiles;
-    const int h = (mb - s_row * htiles) * kRows + wave * kWaveRows + li;
-    row_ok = h < a.h_q;
-    h_row = row_ok ? h : 0;
-    row = s_row * a.h_q + h_row;
+    s_fix = mb / htiles;
+    hbase = (mb - s_fix * htiles) * kRows;
   }
+  // work-group row rho -> (query token s, head hh); false past the last row
+  auto map_row = [&](int rho, int& s, int& hh) -> bool {
+    if constexpr (kMode == kDense) {
+      const int grow = mb * kRows + rho;
+      const bool ok = grow < rows_total;
+      s = ok ? grow / a.h_q : 0;
+      hh = ok ? grow - s * a.h_q : 0;
+      return ok;
+    } else {
+      const int h = hbase + rho;
+      const bool ok = h < a.h_q;
+      s = s_fix;
+      hh = ok ? h : 0;
+      return ok;
+    }
+  };
+  // rows this lane computes S and P for: 32*wave + 16rt + i16
+  int own_s[2], own_h[2];
+  bool own_ok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) own_ok[rt] = map_row(32 * wave + 16 * rt + i16, own_s[rt], own_h[rt]);
+
   const float scale_log2 = a.softmax_scale * kLog2e;
   const float ninf = -__builtin_inff();
   const int topk_pad = (a.topk + kPage - 1) / kPage * kPage;
@@ -349,37 +379,60 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
   const unsigned char* kv = static_cast<const unsigned char*>(a.kv);
   const bf16* q = static_cast<const bf16*>(a.q);
 
-  // ---- per-lane LDS offsets, fixed for the kernel ----
-  // QK A operand (32x32x16): token row li, logical chunk 2k + g of k-step k;
-  // bases by k % 4, k / 4 selects the chunk-group block (+1 KB each).
-  int a_off[4];
-  {
-    const int base = (li >> 3) * kRowGroupBytes + 128 * (li & 7);
+  // ---- per-lane LDS offsets ----
+  // Recomputed at every step from a lane index the compiler cannot see
+  // through (a few VALU ops): kept live across the whole loop they would
+  // cost VGPRs that Q and the pipeline need.
+  struct LaneOffsets {
+    int k[2];   // K operand of QK, by k-step parity
+    int v[4];   // V^T operand of PV, by dim tile % 4
+    int pr;     // P^T operand of PV
+    int pw[2];  // P writes of the softmax, by token tile
+  };
+  auto lane_offsets = [&]() -> LaneOffsets {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int g = ln >> 4, ii = ln & 15;
+    LaneOffsets o;
+    // K operand of QK (A of 16x16x32): token 16tt + ii, logical chunk
+    // 4kq + g of k-step kq.  Bases by kq parity; kq/2 adds one chunk-group
+    // block, tt two row-groups.
+    const int sw = (ii & 7) ^ (ii >> 3);
+    const int kbase = (ii >> 3) * kRowGroupBytes + 128 * (ii & 7);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a_off[j] = base + 16 * ((2 * j + g) ^ swz(li));
-  }
-  // V^T operand of PV (dims 32mt + li, k-step kk): element e is token
-  // 16kk + 8(e/4) + 4g + e%4, the order in which this lane holds P.  Each
-  // transpose read covers 4 tokens: the 16-lane group (g, half16) reads token
-  // rows 16kk + 8h + 4g + c (c = (lane&15)>>2) at dims 32mt + 16 half16 +
-  // 4 qq (qq = lane&3).  Bases by (mt parity, h); kk adds two row-groups and
-  // mt/2 one chunk-group.
-  int v_off[2][2];
-  {
-    const int half16 = (lane >> 4) & 1, c = (lane & 15) >> 2, qq = lane & 3;
-    const int rr = 4 * g + c;  // token row in its row-group
+    for (int par = 0; par < 2; ++par) o.k[par] = kbase + 16 * ((4 * par + g) ^ sw);
+    // V^T operand of PV (A of 16x16x32): dim 128*wave + 16dt + ii, tokens
+    // 8g + 0..7.  Two transpose reads of 4 tokens; in the first, lane 4e + q
+    // of each 16-lane group points at token 8g + e, dims 128*wave + 16dt +
+    // 4q..+3.  Offsets by dt % 4 (dt / 4 adds one chunk-group block); the
+    // second read (tokens 8g + 4..7) is the first one of dim tile dt ^ 2
+    // plus 512.
+    const int e = ii >> 2, qd = ii & 3;
 #pragma unroll
-    for (int mp = 0; mp < 2; ++mp)
+    for (int dt = 0; dt < 4; ++dt)
+      o.v[dt] = (g * kChunkGroups + 2 * wave) * kBlockBytes +
+                16 * (e * 8 + ((2 * dt + (qd >> 1)) ^ e ^ (g & 1))) + 8 * (qd & 1);
+    // P^T operand of PV (B of 16x16x32): row 16rt + ii, tokens 8g..8g+7
+    // (plus rt KB).  The softmax writes row 32*wave + 16rt + ii, tokens
+    // 16tt + 4g..+3 (plus rt KB).
+    const int p_sw = (ii >> 2) & 3;
+    o.pr = ii * 64 + 16 * (g ^ p_sw);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int kl = 4 * mp + 2 * half16 + (qq >> 1);  // logical chunk in its group
-        v_off[mp][h] = h * kRowGroupBytes + 16 * (rr * 8 + (kl ^ rr ^ h)) + 8 * (qq & 1);
-      }
-  }
+    for (int tt = 0; tt < 2; ++tt)
+      o.pw[tt] = (32 * wave + ii) * 64 + 16 * ((2 * tt + (g >> 1)) ^ p_sw) + 8 * (g & 1);
+    return o;
+  };
   // Dense copy lane offset inside a half page: row 8*wave + lrow, chunk
-  // (lane%8) ^ swz(row) of each 128-byte group.
-  const unsigned int page_voff = static_cast<unsigned int>(
-      (8 * wave + lrow) * static_cast<int>(row_stride) + 16 * ((lane & 7) ^ lrow ^ (wave & 1)));
+  // (lane%8) ^ swz(row) of each 128-byte group (recomputed where used, like
+  // the LDS offsets).
+  auto page_voff = [&]() -> unsigned int {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int lr = ln >> 3;
+    return static_cast<unsigned int>((8 * wave + lr) * static_cast<int>(row_stride) +
+                                     16 * ((ln & 7) ^ lr ^ (wave & 1)));
+  };
+  const int f8_p = lane & 7;  // fp8: eighth of tile row 8*wave + lrow
 
   // Metadata from another batch / topk must not drive accesses out of bounds:
   // sequence, block and split indices are clamped to this call's shapes.
@@ -400,55 +453,52 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     const int ns0 = sload(a.num_splits + b);
     const int nsplit = sload(a.num_splits + b + 1) - ns0;
     const bool split_ok = ns0 >= 0 && split_local >= 0 && ns0 + split_local < max_split;
-    // Keys this row may see (dense, bottom-right causal), relative to the
-    // segment start; tiles from causal_from on need the per-row check.
-    const int row_limit =
-        ((kMode == kDense && a.causal) ? seqlen - a.s_q + 1 + s_row : seqlen) - tok_lo;
+    // Keys owned row rt may see (dense, bottom-right causal), relative to
+    // the segment start; tiles from causal_from on need the per-row check.
+    auto row_limit = [&](int rt) -> int {
+      return ((kMode == kDense && a.causal) ? seqlen - a.s_q + 1 + own_s[rt] : seqlen) - tok_lo;
+    };
     const int causal_from =
         (kMode == kDense && a.causal) ? (seqlen - a.s_q + 1 - tok_lo) / kTileRows : ntiles;
     const int32_t* bt = a.block_table + static_cast<long long>(b) * a.bt_stride_b;
     const int32_t* srows =
         kMode == kDense ? nullptr
-                        : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s_row) * topk_pad;
+                        : a.sparse_rows + (static_cast<long long>(b) * a.s_q + s_fix) * topk_pad;
 
-    // ---- Q^T operand: dims 16k + 8g .. +7 of this lane's row ----
-    // k < kQRegs in VGPRs (qf), the last k-steps in this wave's LDS slot
-    // (qx): the register file is full (O accumulators + Q + the pipeline).
-    bf16x8 qf[kQRegs];
-    {
-      bf16x8 qrest[kQSteps - kQRegs];
-      if (row_ok) {
-        const bf16* qrow =
-            q + b * a.q_stride_b + s_row * a.q_stride_s + h_row * a.q_stride_h + 8 * g;
+    // ---- Q^T operand j = 2kq + rt: row 32*wave + 16rt + i16, dims 32kq + 8G..+7 ----
+    // The first kQLds operands sit in this wave's LDS slot (read at the start
+    // of each QK, with the first K operands): the VGPRs hold the rest of Q
+    // and the pipeline, the AGPRs the O accumulators.  The LDS part goes
+    // there directly (LDS-destination loads, 16 bytes per lane = the slot's
+    // lane layout); all of it is waited for only behind the first tile
+    // requests.  Rows past the last one read the zero row.
+    bf16x8 qf[kQOps - kQLds];
 #pragma unroll
-        for (int k = 0; k < kQRegs; ++k) qf[k] = *reinterpret_cast<const bf16x8*>(qrow + 16 * k);
+    for (int rt = 0; rt < 2; ++rt) {
+      const bf16* qrow =
+          own_ok[rt] ? q + b * a.q_stride_b + own_s[rt] * a.q_stride_s + own_h[rt] * a.q_stride_h + 8 * G
+                     : reinterpret_cast<const bf16*>(g_zero_row);
 #pragma unroll
-        for (int k = kQRegs; k < kQSteps; ++k)
-          qrest[k - kQRegs] = *reinterpret_cast<const bf16x8*>(qrow + 16 * k);
-      } else {
-#pragma unroll
-        for (int k = 0; k < kQRegs; ++k) qf[k] = bf16x8{};
-#pragma unroll
-        for (int k = kQRegs; k < kQSteps; ++k) qrest[k - kQRegs] = bf16x8{};
+      for (int kq = 0; kq < kQkSteps; ++kq) {
+        const int j = 2 * kq + rt;
+        if (j >= kQLds) {
+          qf[j - kQLds] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kq);
+        } else {
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(qrow + 32 * kq),
+                                           (FA_LDS void*)(&sm.qx[wave][j][0]), 16, 0, 0);
+        }
       }
-#pragma unroll
-      for (int k = kQRegs; k < kQSteps; ++k)
-        *reinterpret_cast<bf16x8*>(sm.qx[wave][k - kQRegs] + 16 * lane) = qrest[k - kQRegs];
     }
-    auto q_op = [&](int k) -> bf16x8 {
-      return k < kQRegs ? qf[k]
-                        : *reinterpret_cast<const bf16x8*>(sm.qx[wave][k - kQRegs] + 16 * lane);
+    auto q_op = [&](int j) -> bf16x8 {
+      return j >= kQLds ? qf[j - kQLds] : sm.qx[wave][j][lane];
     };
 
-    // ---- tile producers (wave w fills row-group w of every tile) ----
-    // bf16 tiles go HBM -> LDS directly, requested three tiles ahead (two
-    // steps of latency slack).  fp8 tiles are loaded into registers three
-    // tiles ahead and dequantised into LDS two tiles ahead.  Every lane
-    // issues the same loads for every tile (masked rows / pages read zeros),
-    // so the vmcnt waits are constants.
-    // dense: page of the block of the next tile to request, looked up at the
-    // end of the previous step (the scalar load completes at the barrier
-    // that starts the next step)
+    // ---- tile producers ----
+    // bf16 tiles go HBM -> LDS directly, requested two tiles ahead.  fp8
+    // tiles are loaded into registers three tiles ahead and dequantised into
+    // LDS two tiles ahead.  Every lane issues the same loads for every tile
+    // (masked rows / pages read zeros), so the vmcnt waits are constants.
+    // dense: page of the next tile to request, looked up one step ahead
     int next_page = -1;
     auto prefetch_page = [&](int u) {
       if ((u & 1) == 0) {
@@ -458,330 +508,398 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     };
     // dense: buffer resource of tile u's half page (rows past the sequence,
     // or a page id outside the cache, read as zeros) and its key mask
-    auto dense_prep = [&](int u) -> __amdgpu_buffer_rsrc_t {
+    // A tile request: this wave's nine 1 KB blocks of the tile, issued one
+    // at a time (copy_block) so that the address work of the requests runs
+    // beside the MFMAs instead of stalling every wave at once.
+    struct CopyReq {
+      __amdgpu_buffer_rsrc_t rs;  // dense: the half page
+      const unsigned char* src;   // sparse bf16: this lane's source row chunk
+      unsigned int voff;          // dense: this lane's offset in the half page
+      unsigned char* dst;         // this wave's row-group of the tile buffer
+    };
+    auto copy_block = [&](const CopyReq& c, auto gt) {
+      constexpr int Gc = decltype(gt)::value;
+      if constexpr (kMode == kDense) {
+        copy_block_buf<Gc>(c.rs, c.dst, c.voff);
+      } else if constexpr (kMode == kSparseBf16) {
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(c.src + 128 * Gc),
+                                         (FA_LDS void*)(c.dst + Gc * kBlockBytes), 16, 0, 0);
+      }
+    };
+    auto copy_all = [&](const CopyReq& c) {
+      static_for<kChunkGroups>([&](auto gt) { copy_block(c, gt); });
+    };
+    // dense: request of tile u's half page (rows past the sequence, or a page
+    // id outside the cache, read as zeros); *mask = its key mask
+    auto dense_req = [&](int u, unsigned char* buf, unsigned int* mask) -> CopyReq {
       const int blk = blk_lo + (u >> 1), half = u & 1;
       const bool ok = u < ntiles && next_page >= 0 && next_page < a.num_kv_blocks;
       const int start = blk * kPage + kTileRows * half;
       const int nrows = ok ? max(0, min(seqlen - start, kTileRows)) : 0;
       const unsigned char* base =
           kv + (ok ? next_page : 0) * block_stride + kTileRows * half * row_stride;
-      if (tid == 0)
-        sm.vmask[u & (kSlots - 1)] = nrows >= kTileRows ? ~0u : ((1u << nrows) - 1u);
-      return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(uniform(base)), 0,
+      CopyReq c;
+      c.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(uniform(base)), 0,
                                                uniform(nrows * static_cast<int>(row_stride)),
                                                0x00020000);
+      c.src = nullptr;
+      c.voff = page_voff();
+      c.dst = buf + wave * kRowGroupBytes;
+      *mask = nrows >= kTileRows ? ~0u : ((1u << nrows) - 1u);
+      return c;
     };
-    auto dense_issue = [&](int u, unsigned char* buf) {
-      const __amdgpu_buffer_rsrc_t rs = dense_prep(u);
-      unsigned char* dst = buf + wave * kRowGroupBytes;
-      static_for<kChunkGroups>([&](auto gt) {
-        copy_block_buf<decltype(gt)::value>(rs, dst, page_voff);
-      });
-    };
-    // sparse: physical row of this lane's tile row for tile u (-1: masked)
+    // sparse: physical row of tile row (lane % 32) of tile u (-1: masked)
+    // sparse: physical row of tile row (lane % 32) of tile u, as loaded
+    // (the tile index is clamped so the load stays inside the row list);
+    // row_valid masks tiles past the end (-1: masked).  The select waits for
+    // the load, so it is applied only where the row is used.
     auto load_row = [&](int u) -> int32_t {
       const int uu = u < ntiles ? u : ntiles - 1;
-      const int32_t r = srows[(tok_lo + kTileRows * uu) + 8 * wave + lrow];
-      return u < ntiles ? r : -1;
+      return srows[(tok_lo + kTileRows * uu) + (lane & 31)];
     };
+    auto row_valid = [&](int u, int32_t r) -> int32_t { return u < ntiles ? r : -1; };
     auto row_ptr = [&](int32_t r) -> const unsigned char* {
       return r >= 0 ? kv + static_cast<long long>(r >> 6) * block_stride +
                           static_cast<long long>(r & 63) * row_stride
                     : static_cast<const unsigned char*>(g_zero_row);
     };
-    auto publish_mask = [&](int u, int32_t r) {  // wave w owns byte w of tile u's mask
-      const unsigned long long bal = __ballot(r >= 0);
-      unsigned int byte = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) byte |= static_cast<unsigned int>((bal >> (8 * j)) & 1ull) << j;
-      if (lane == 0)
-        reinterpret_cast<unsigned char*>(sm.vmask)[(u & (kSlots - 1)) * 4 + wave] =
-            static_cast<unsigned char>(byte);
+    // sparse: key mask of a tile from its rows (lanes 0..31 hold rows 0..31)
+    auto row_mask = [&](int32_t r) -> unsigned int {
+      return static_cast<unsigned int>(__ballot(r >= 0));
     };
-    int32_t row_next = -1;  // sparse: row for the next tile to request
+    // sparse bf16: gathered rows (r = the rows of lanes 0..31)
+    auto gather_req = [&](int32_t r, unsigned char* buf) -> CopyReq {
+      CopyReq c;
+      c.rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
+      c.src = row_ptr(__shfl(r, 8 * wave + lrow)) + 16 * ((lane & 7) ^ lrow ^ (wave & 1));
+      c.voff = 0;
+      c.dst = buf + wave * kRowGroupBytes;
+      return c;
+    };
+    int32_t rq0 = -1, rq1 = -1;  // sparse: rows of tiles t+2 and t+3 (fp8: t+3)
+    // key masks of tiles t.. (scalar queue; bit j: token j of the tile)
+    unsigned int vq[3] = {0u, 0u, 0u};
     Fp8Slice f8;
-    const int f8_p = lane & 7;
 
-    // ---- online softmax of this lane's row (log2 units) ----
-    // The reference mref that P and the accumulators are relative to is set
-    // by the first tile with a visible key and then kept: a later score
-    // above it only makes P > 1, harmless while S - mref stays below
-    // kHeadroom (P, the row sum and the accumulators stay far inside the fp32
-    // / bf16 range).  So the accumulators are never rescaled.  If some score
-    // climbs past mref + kHeadroom (scores spread over > 2^64), the sequence
-    // is processed again with mref preset to the row max found.
+    // ---- softmax state of the two owned rows (log2 units) ----
     constexpr float kHeadroom = 64.f;
-    float mref, mmax, lsum;
+    float mref[2], mmax[2], lsum[2];
     bool overflow;
-    floatx16 acc[kDimTiles];
+    floatx4 acc[kDimTiles][kRowTiles];
 
-    auto qk_read = [&](const unsigned char* kb, int k) -> bf16x8 {
-      return *reinterpret_cast<const bf16x8*>(kb + a_off[k & 3] + (k >> 2) * kBlockBytes);
+    auto k_read = [&](const LaneOffsets& lo, const unsigned char* kb, int kq, int tt) -> bf16x8 {
+      return *reinterpret_cast<const bf16x8*>(kb + lo.k[kq & 1] + (kq >> 1) * kBlockBytes +
+                                              tt * 2 * kRowGroupBytes);
     };
-    // V^T operand of PV MFMA j (kk = j / 16, mt = j % 16): two transpose reads
-    auto v_read = [&](const unsigned char* kb, int j) -> bf16x8 {
-      const int kk = j >> 4, mt = j & 15;
-      const unsigned char* p = kb + kk * 2 * kRowGroupBytes + (mt >> 1) * kBlockBytes;
-      const bf16x4 lo = lds_read_tr4(p + v_off[mt & 1][0]);
-      const bf16x4 hi = lds_read_tr4(p + v_off[mt & 1][1]);
-      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    // Softmax of tile u from its S: P^T operands (pk[kk] = the tokens of
-    // k-step kk in this lane's order).
-    auto softmax = [&](int u, unsigned int vm, const floatx16& sacc, bf16x8 (&pk)[2]) {
-      float sv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sv[r] = sacc[r] * scale_log2;
-      if (vm != ~0u || u >= causal_from) {  // partial tile (uniform branch)
-        // token 8(r/4) + 4g + r%4 of the tile: bit c_r = 8(r/4) + r%4 of
-        // vm >> 4g, visible while c_r < row_limit - 32u - 4g
-        const unsigned int vmg = vm >> (4 * g);
-        const int lim = row_limit - kTileRows * u - 4 * g;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = 8 * (r >> 2) + (r & 3);
-          const bool ok = ((vmg >> c) & 1u) && c < lim;
-          sv[r] = ok ? sv[r] : ninf;
-        }
-      }
-      float m = sv[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) m = fmaxf(m, sv[r]);
-      m = max_xor32(m);  // the row's max over the 32 tokens
-      mref = mref == ninf ? m : mref;
-      mmax = fmaxf(mmax, m);
-      overflow = overflow | (m > mref + kHeadroom);
-      const float mu = mref == ninf ? 0.f : mref;
-      float ps = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sv[r] = __builtin_amdgcn_exp2f(sv[r] - mu);
-        ps += sv[r];
-      }
-      lsum += ps;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        uintx4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(sv[8 * kk + 2 * i], sv[8 * kk + 2 * i + 1]);
-        pk[kk] = __builtin_bit_cast(bf16x8, w);
-      }
+    auto v_read = [&](const LaneOffsets& lo, const unsigned char* kb, int dt) -> bf16x8 {
+      const unsigned char* p = kb + (dt >> 2) * kBlockBytes;
+      const bf16x4 l4 = lds_read_tr4(p + lo.v[dt & 3]);
+      const bf16x4 h4 = lds_read_tr4(p + lo.v[(dt & 3) ^ 2] + 512);
+      return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
-    if (tid == 0) sm.redo = 0u;
-    float mref_start = ninf;
+    float mref_start[2] = {ninf, ninf};
     for (int pass = 0;; ++pass) {
-      mref = mref_start;
-      mmax = ninf;
-      lsum = 0.f;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        mref[rt] = mref_start[rt];
+        mmax[rt] = ninf;
+        lsum[rt] = 0.f;
+      }
       overflow = false;
 #pragma unroll
-      for (int i = 0; i < kDimTiles; ++i) acc[i] = floatx16{};
+      for (int dt = 0; dt < kDimTiles; ++dt)
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) acc[dt][rt] = floatx4{};
 
-      // ---- prologue: tiles 0..2 requested, tile 0 through QK ----
+      // ---- prologue: tiles 0 and 1 requested ----
       if constexpr (kMode == kDense) {
         prefetch_page(0);
-        dense_issue(0, kv_buf0);
-        dense_issue(1, kv_buf1);
+        copy_all(dense_req(0, kv_buf0, &vq[0]));
+        prefetch_page(1);
+        copy_all(dense_req(1, kv_buf1, &vq[1]));
         prefetch_page(2);
-        dense_issue(2, kv_buf2);
-        wait_vmem<18>();
       } else if constexpr (kMode == kSparseBf16) {
-        const int32_t r0 = load_row(0), r1 = load_row(1), r2 = load_row(2);
+        const int32_t r0l = load_row(0), r1l = load_row(1);
         wait_vmem<0>();
-        copy_gather_row(kv_buf0, wave, row_ptr(r0));
-        publish_mask(0, r0);
-        copy_gather_row(kv_buf1, wave, row_ptr(r1));
-        publish_mask(1, r1);
-        row_next = load_row(3);
-        copy_gather_row(kv_buf2, wave, row_ptr(r2));
-        publish_mask(2, r2);
-        wait_vmem<18>();  // whatever order the row load took
+        const int32_t r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
+        vq[0] = row_mask(r0);
+        vq[1] = row_mask(r1);
+        // issue order copies(0), rows(2), copies(1), rows(3): the order the
+        // steps keep (rows two tiles before their copies)
+        copy_all(gather_req(r0, kv_buf0));
+        rq0 = load_row(2);
+        copy_all(gather_req(r1, kv_buf1));
+        rq1 = load_row(3);
       } else {
         int32_t r = load_row(0);
         wait_vmem<0>();
-        load_fp8_slice(f8, row_ptr(r), f8_p);
-        publish_mask(0, r);
-        r = load_row(1);
+        r = row_valid(0, r);
+        vq[0] = row_mask(r);
+        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
+        r = row_valid(1, load_row(1));
         wait_vmem<0>();
         store_fp8_slice(kv_buf0, f8, 8 * wave + lrow, f8_p);
-        load_fp8_slice(f8, row_ptr(r), f8_p);
-        publish_mask(1, r);
-        r = load_row(2);
+        vq[1] = row_mask(r);
+        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
+        r = row_valid(2, load_row(2));
         wait_vmem<0>();
         store_fp8_slice(kv_buf1, f8, 8 * wave + lrow, f8_p);
-        load_fp8_slice(f8, row_ptr(r), f8_p);
-        publish_mask(2, r);
-        row_next = load_row(3);
-      }
-      barrier();
-      floatx16 scur = floatx16{};  // S^T of the tile the next step turns into P
-      {
-        bf16x8 af[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) af[k] = qk_read(kv_buf0, k);
-#pragma unroll
-        for (int k = 0; k < kQSteps; ++k) {
-          const bf16x8 cur = af[k & 3];
-          if (k + 4 < kQSteps) af[k & 3] = qk_read(kv_buf0, k + 4);
-          mfma32_vacc(cur, q_op(k), scur);
-        }
+        vq[2] = row_mask(r);
+        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
+        rq0 = load_row(3);
       }
 
-      // ---- step t: QK(t+1) with softmax(t) under it, then PV(t) ----
+      // ---- step t: QK(t), softmax(t) -> P | PV(t) ----
       auto step = [&](const int t, auto tag) {
-        constexpr int K = decltype(tag)::value;  // t % 4
-        unsigned char* const b_pv = FA_KVBUF(K);
-        unsigned char* const b_qk = FA_KVBUF((K + 1) & 3);
-        unsigned char* const b_f8 = FA_KVBUF((K + 2) & 3);
-        unsigned char* const b_cp = FA_KVBUF((K + 3) & 3);
-        // this wave's copies of tile t+1 landed (tile t+2's may still be in
-        // flight), then everyone's; everyone is done with step t-1, which
-        // frees buffer (t+3) % 4
+        constexpr int K = decltype(tag)::value;  // t % 3
+        unsigned char* const b_cur = FA_KVBUF(K);
+        unsigned char* const b_cp = FA_KVBUF((K + 2) % 3);
+        // this wave's copies of tile t landed (those of t+1 may be in flight),
+        // then everyone's; everyone is done with step t-1, which frees buffer
+        // (t+2) % 3
         if constexpr (kMode == kSparseFp8) {
           wait_vmem<0>();
+        } else if constexpr (kMode == kSparseBf16) {
+          wait_vmem<kCopiesPerWave + 1>();  // also the rows of tile t+2
         } else {
           wait_vmem<kCopiesPerWave>();
         }
         barrier();
-        __amdgpu_buffer_rsrc_t rs;               // dense requests
-        const unsigned char* gsrc = g_zero_row;  // sparse bf16 requests
+        const unsigned int vm = vq[0];
+        const LaneOffsets lo = lane_offsets();
+        CopyReq creq;  // tile t+2, issued block by block during QK(t)
         if constexpr (kMode == kDense) {
-          rs = dense_prep(t + 3);
+          unsigned int m;
+          creq = dense_req(t + 2, b_cp, &m);
+          vq[0] = vq[1];
+          vq[1] = m;
+        } else if constexpr (kMode == kSparseBf16) {
+          const int32_t r = row_valid(t + 2, rq0);
+          rq0 = rq1;
+          rq1 = load_row(t + 4);  // before the copies: a later wait covers it
+          creq = gather_req(r, b_cp);
+          vq[0] = vq[1];
+          vq[1] = row_mask(r);
         } else {
-          rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
+          store_fp8_slice(b_cp, f8, 8 * wave + lrow, f8_p);
+          const int32_t r = row_valid(t + 3, rq0);
+          load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
+          rq0 = load_row(t + 4);
+          vq[0] = vq[1];
+          vq[1] = vq[2];
+          vq[2] = row_mask(r);
         }
-        if constexpr (kMode == kSparseBf16) {
-          const int32_t r = row_next;
-          row_next = load_row(t + 4);
-          gsrc = row_ptr(r) + 16 * ((lane & 7) ^ lrow ^ (wave & 1));
-          publish_mask(t + 3, r);
-        } else if constexpr (kMode == kSparseFp8) {
-          store_fp8_slice(b_f8, f8, 8 * wave + lrow, f8_p);
-          load_fp8_slice(f8, row_ptr(row_next), f8_p);
-          publish_mask(t + 3, row_next);
-          row_next = load_row(t + 4);
-        }
-        const unsigned int vm = sm.vmask[t & (kSlots - 1)];
-        unsigned char* const dst = b_cp + wave * kRowGroupBytes;
         __builtin_amdgcn_sched_barrier(0);
 
-        // QK(t+1): 36 MFMAs, K reads 4 ahead, one tile request every 4
-        // MFMAs, the softmax of tile t (VALU) between them
-        floatx16 snext = floatx16{};
-        bf16x8 pk[2];
-        softmax(t, vm, scur, pk);
+        // QK(t): S of rows 32*wave.. for the 32 tokens, 72 MFMAs in four
+        // independent accumulator chains (token tile tt x row tile rt).  K
+        // operands are read kPre k-steps ahead; the fences keep the reads
+        // ahead of the MFMAs that the compiler cannot see into.
+        floatx4 sacc[2][2];
         {
-          bf16x8 af[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) af[k] = qk_read(b_qk, k);
-          static_for<kQSteps>([&](auto kt) {
-            constexpr int k = decltype(kt)::value;
-            const bf16x8 cur = af[k & 3];
-            if constexpr (k + 4 < kQSteps) af[k & 3] = qk_read(b_qk, k + 4);
-            mfma32_vacc(cur, q_op(k), snext);
-            if constexpr ((k & 3) == 0 && (k >> 2) < kChunkGroups) {
-              constexpr int G = k >> 2;
-              if constexpr (kMode == kDense) {
-                copy_block_buf<G>(rs, dst, page_voff);
-              } else if constexpr (kMode == kSparseBf16) {
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(gsrc + 128 * G),
-                                                 (FA_LDS void*)(dst + G * kBlockBytes), 16, 0, 0);
-              }
+          constexpr int kPre = kMode == kDense ? 1 : 2, kRing = kPre + 1;
+          bf16x8 ka[kRing][2];
+          static_for<kPre>([&](auto pt) {
+            constexpr int kq = decltype(pt)::value;
+            ka[kq][0] = k_read(lo, b_cur, kq, 0);
+            ka[kq][1] = k_read(lo, b_cur, kq, 1);
+          });
+          static_for<kQkSteps>([&](auto kt) {
+            constexpr int kq = decltype(kt)::value;
+            if constexpr (kq + kPre < kQkSteps) {
+              ka[(kq + kPre) % kRing][0] = k_read(lo, b_cur, kq + kPre, 0);
+              ka[(kq + kPre) % kRing][1] = k_read(lo, b_cur, kq + kPre, 1);
             }
+            const bf16x8 q0 = q_op(2 * kq), q1 = q_op(2 * kq + 1);
+            if constexpr (kMode != kSparseFp8 && (kq & 1) == 0 && (kq >> 1) < kChunkGroups)
+              copy_block(creq, IntTag<(kq >> 1)>{});
+            __builtin_amdgcn_sched_barrier(0);
+            const bf16x8 a0 = ka[kq % kRing][0], a1 = ka[kq % kRing][1];
+            if constexpr (kq == 0) {
+              mfma16_vacc_first(a0, q0, sacc[0][0]);
+              mfma16_vacc_first(a0, q1, sacc[0][1]);
+              mfma16_vacc_first(a1, q0, sacc[1][0]);
+              mfma16_vacc_first(a1, q1, sacc[1][1]);
+            } else {
+              mfma16_vacc(a0, q0, sacc[0][0]);
+              mfma16_vacc(a0, q1, sacc[0][1]);
+              mfma16_vacc(a1, q0, sacc[1][0]);
+              mfma16_vacc(a1, q1, sacc[1][1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
           });
+          mfma_vacc_drain(sacc);
         }
+
+        // V^T operands of PV(t), read now so that the softmax hides them
+        bf16x8 va[kDimTiles];
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) va[dt] = v_read(lo, b_cur, dt);
         __builtin_amdgcn_sched_barrier(0);
 
-        // PV(t): 32 MFMAs, V^T reads kVPre MFMAs ahead
-        constexpr int kVPre = 3;
-        {
-          bf16x8 vq[kVPre];
+        // softmax(t) of the owned rows: row 32*wave + 16rt + i16, tokens
+        // 16tt + 4G + i (8 per row and lane)
 #pragma unroll
-          for (int j = 0; j < kVPre; ++j) vq[j] = v_read(b_pv, j);
-          static_for<2 * kDimTiles>([&](auto jt) {
-            constexpr int j = decltype(jt)::value;
-            const bf16x8 av = vq[j % kVPre];
-            if constexpr (j + kVPre < 2 * kDimTiles) vq[j % kVPre] = v_read(b_pv, j + kVPre);
-            acc[j & 15] = mfma32(av, pk[j >> 4], acc[j & 15]);
-          });
-          __builtin_amdgcn_sched_group_barrier(0x100, 2 * kVPre, 0);
-          static_for<2 * kDimTiles>([&](auto jt) {
-            constexpr int j = decltype(jt)::value;
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if constexpr (j + kVPre < 2 * kDimTiles)
-              __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        for (int rt = 0; rt < 2; ++rt) {
+          float sv[8];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[4 * tt + i] = sacc[tt][rt][i] * scale_log2;
+          if (vm != ~0u || t >= causal_from) {  // partial tile (uniform branch)
+            const unsigned int vmg = vm >> (4 * G);
+            const int lim = row_limit(rt) - kTileRows * t - 4 * G;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int c = 16 * tt + i;
+                const bool ok = ((vmg >> c) & 1u) && c < lim;
+                sv[4 * tt + i] = ok ? sv[4 * tt + i] : ninf;
+              }
+          }
+          // this lane's running max: the overflow check and the second
+          // pass's reference are taken from it at the end of the pass
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mmax[rt] = fmaxf(mmax[rt], sv[i]);
+          // the reference: the row max of the first tile with a visible key
+          if (__ballot(mref[rt] == ninf) != 0ull) {  // uniform; rare
+            float m = sv[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) m = fmaxf(m, sv[i]);
+            m = max_xor32(max_xor16(m));
+            mref[rt] = mref[rt] == ninf ? m : mref[rt];
+          }
+          const float mu = mref[rt] == ninf ? 0.f : mref[rt];
+          float ps = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            sv[i] = __builtin_amdgcn_exp2f(sv[i] - mu);
+            ps += sv[i];
+          }
+          lsum[rt] += ps;
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            uintx2 w;
+            w[0] = pack_bf16x2(sv[4 * tt + 0], sv[4 * tt + 1]);
+            w[1] = pack_bf16x2(sv[4 * tt + 2], sv[4 * tt + 3]);
+            *reinterpret_cast<uintx2*>(sm.p + lo.pw[tt] + rt * 1024) = w;
+          }
+        }
+        barrier();
+
+        // PV(t): dims 128*wave.. of all 128 rows, 64 MFMAs; P^T read two row
+        // tiles ahead
+        {
+#pragma unroll
+          for (int dt = 2; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
+          bf16x8 pb[2];
+          auto p_read = [&](int rt) -> bf16x8 {
+            return *reinterpret_cast<const bf16x8*>(sm.p + lo.pr + rt * 1024);
+          };
+          pb[0] = p_read(0);
+          static_for<kRowTiles>([&](auto rtt) {
+            constexpr int rt = decltype(rtt)::value;
+            if constexpr (rt + 1 < kRowTiles) pb[(rt + 1) % 2] = p_read(rt + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int dt = 0; dt < kDimTiles; ++dt) mfma16_aacc(va[dt], pb[rt % 2], acc[dt][rt]);
+            __builtin_amdgcn_sched_barrier(0);
           });
         }
-        scur = snext;
-        if constexpr (kMode == kDense) prefetch_page(t + 4);
+        if constexpr (kMode == kDense) prefetch_page(t + 3);  // lands by the next barrier
       };
-      // Whole rounds of four steps, then the remainder (the loop back-edge
-      // is only taken after step 3, which keeps the compiler's view of the
+      // Whole rounds of three steps, then the remainder (the loop back-edge
+      // is only taken after step 2, which keeps the compiler's view of the
       // buffers the same on every iteration).
       int t = 0;
-      for (; t + 4 <= ntiles; t += 4) {
+      for (; t + 3 <= ntiles; t += 3) {
         step(t, IntTag<0>{});
         step(t + 1, IntTag<1>{});
         step(t + 2, IntTag<2>{});
-        step(t + 3, IntTag<3>{});
       }
       if (t < ntiles) {
         step(t, IntTag<0>{});
-        if (t + 1 < ntiles) {
-          step(t + 1, IntTag<1>{});
-          if (t + 2 < ntiles) step(t + 2, IntTag<2>{});
-        }
+        if (t + 1 < ntiles) step(t + 1, IntTag<1>{});
       }
       wait_vmem<0>();  // requests for tiles past the end land before LDS is reused
-      if (pass > 0) break;
-      if (__any(overflow) && lane == 0) sm.redo = 1u;
+      if (pass > 0) {
+        barrier();  // every wave is past its last PV: the P buffer is free
+        break;
+      }
+      // second pass if any row of the work-group overflowed: per-wave flags
+      // in the P buffer, free once every wave is past its last PV
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        mmax[rt] = max_xor32(max_xor16(mmax[rt]));  // the row max
+        overflow = overflow | (mmax[rt] > mref[rt] + kHeadroom);
+      }
       barrier();
-      if (sm.redo == 0u) break;
-      mref_start = mmax;  // second pass (rare): the row max is known
+      unsigned int* const flags = reinterpret_cast<unsigned int*>(sm.p + 4096);
+      if (lane == 0) flags[wave] = __any(overflow) ? 1u : 0u;
+      barrier();
+      if ((flags[0] | flags[1] | flags[2] | flags[3]) == 0u) break;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) mref_start[rt] = mmax[rt];  // second pass (rare)
     }
 
-    // ---- epilogue: normalise, write out / partials ----
-    const float l = sum_xor32(lsum);
-    if (row_ok) {
+    mfma_drain();  // the last PV MFMAs complete before the accumulators are read
+
+    // ---- epilogue: owners publish the row sums; every wave normalises its dims ----
+    float l_own[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      l_own[rt] = sum_xor32(sum_xor16(lsum[rt]));
+      if (G == 0) reinterpret_cast<float*>(sm.p)[32 * wave + 16 * rt + i16] = l_own[rt];
+    }
+    barrier();
+    const long long pbase = static_cast<long long>(ns0 + split_local) * rows_total;
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      // computed here, per sequence: hoisting these row indices out of the
+      // sequence loop would keep 8 of them live through the whole kernel
+      int rho = 16 * rt + i16;
+      asm volatile("" : "+v"(rho));
+      int s, hh;
+      const bool ok = map_row(rho, s, hh);
+      const float l = reinterpret_cast<const float*>(sm.p)[rho];
       const float inv = l > 0.f ? 1.f / l : 0.f;
-      const float lse_v = l > 0.f ? (mref + log2f(l)) * kLn2 : ninf;
-      const int dim0 = 4 * g;  // + 32 mt + 8 qd (+0..3): acc[mt][4qd + i]
-      if (nsplit == 1) {
+      const int dim0 = 128 * wave + 4 * G;  // + 16 dt + i
+      if (ok && nsplit == 1) {
         bf16* orow = static_cast<bf16*>(a.out) +
-                     ((static_cast<long long>(b) * a.s_q + s_row) * a.h_q + h_row) * kDv + dim0;
+                     ((static_cast<long long>(b) * a.s_q + s) * a.h_q + hh) * kDv + dim0;
 #pragma unroll
-        for (int mt = 0; mt < kDimTiles; ++mt) {
-#pragma unroll
-          for (int qd = 0; qd < 4; ++qd) {
-            uintx2 w;
-            w[0] = pack_bf16x2(acc[mt][4 * qd + 0] * inv, acc[mt][4 * qd + 1] * inv);
-            w[1] = pack_bf16x2(acc[mt][4 * qd + 2] * inv, acc[mt][4 * qd + 3] * inv);
-            *reinterpret_cast<uintx2*>(orow + 32 * mt + 8 * qd) = w;
-          }
-          __builtin_amdgcn_sched_barrier(0);
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          uintx2 w;
+          w[0] = pack_bf16x2(acc[dt][rt][0] * inv, acc[dt][rt][1] * inv);
+          w[1] = pack_bf16x2(acc[dt][rt][2] * inv, acc[dt][rt][3] * inv);
+          *reinterpret_cast<uintx2*>(orow + 16 * dt) = w;
         }
-        if (g == 0) a.lse[(static_cast<long long>(b) * a.h_q + h_row) * a.s_q + s_row] = lse_v;
-      } else if (split_ok) {
-        const long long prow = static_cast<long long>(ns0 + split_local) * rows_total + row;
-        float* orow = a.o_accum + prow * kDv + dim0;
+      } else if (ok && split_ok) {
+        bf16* orow = static_cast<bf16*>(a.o_accum) + (pbase + s * a.h_q + hh) * kDv + dim0;
 #pragma unroll
-        for (int mt = 0; mt < kDimTiles; ++mt) {
-#pragma unroll
-          for (int qd = 0; qd < 4; ++qd) {
-            floatx4 w;
-            w[0] = acc[mt][4 * qd + 0] * inv;
-            w[1] = acc[mt][4 * qd + 1] * inv;
-            w[2] = acc[mt][4 * qd + 2] * inv;
-            w[3] = acc[mt][4 * qd + 3] * inv;
-            *reinterpret_cast<floatx4*>(orow + 32 * mt + 8 * qd) = w;
-          }
-          __builtin_amdgcn_sched_barrier(0);
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          uintx2 w;
+          w[0] = pack_bf16x2(acc[dt][rt][0] * inv, acc[dt][rt][1] * inv);
+          w[1] = pack_bf16x2(acc[dt][rt][2] * inv, acc[dt][rt][3] * inv);
+          *reinterpret_cast<uintx2*>(orow + 16 * dt) = w;
         }
-        if (g == 0) a.lse_accum[prow] = lse_v;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      if (own_ok[rt] && G == 0) {
+        const float lse_v = l_own[rt] > 0.f ? (mref[rt] + log2f(l_own[rt])) * kLn2 : ninf;
+        if (nsplit == 1) {
+          a.lse[(static_cast<long long>(b) * a.h_q + own_h[rt]) * a.s_q + own_s[rt]] = lse_v;
+        } else if (split_ok) {
+          a.lse_accum[pbase + own_s[rt] * a.h_q + own_h[rt]] = lse_v;
+        }
       }
     }
-    barrier();  // LDS (tiles, masks) is reused by the next sequence
+    barrier();  // LDS (tiles, masks, row sums) is reused by the next sequence
   }
 #undef FA_KVBUF
 }

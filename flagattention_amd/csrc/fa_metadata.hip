@@ -26,19 +26,22 @@ constexpr int kMetaThreads = 256;
 constexpr int kMaxB = FA_MLA_MAX_BATCH;
 constexpr int kMaxP = FA_MLA_MAX_PARTS;
 
-// Inclusive prefix sum over the work-group (one value per thread).
+// Inclusive prefix sum over the work-group (one value per thread): a
+// shuffle scan inside each wave, then the wave totals (two barriers in all;
+// `sh` holds one total per wave and is free again on return).
 __device__ long long block_incl_scan(long long v, long long* sh) {
-  const int t = threadIdx.x;
-  sh[t] = v;
-  __syncthreads();
-  for (int off = 1; off < kMetaThreads; off <<= 1) {
-    long long x = (t >= off) ? sh[t - off] : 0;
-    __syncthreads();
-    v += x;
-    sh[t] = v;
-    __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const long long x = __shfl_up(v, off);
+    if (lane >= off) v += x;
   }
-  return v;
+  if (lane == 63) sh[w] = v;
+  __syncthreads();
+  long long base = 0;
+  for (int i = 0; i < w; ++i) base += sh[i];
+  __syncthreads();
+  return v + base;
 }
 
 // Largest i in [0, n) with a[i] <= x (a non-decreasing, a[0] <= x).

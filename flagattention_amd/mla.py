@@ -199,7 +199,7 @@ class DecodeWorkspace:
     ``flash_mla_with_kvcache`` builds a transient one per call; a serving loop (or a
     benchmark) can keep one and call :meth:`run` every step, so no allocation happens
     per step.  Buffers: ``out`` bf16 [B, s_q, h_q, 512], ``lse`` fp32 [B, h_q, s_q],
-    ``o_accum`` fp32 [B + parts, s_q * h_q, 512], ``lse_accum`` fp32 [B + parts, s_q * h_q]
+    ``o_accum`` bf16 [B + parts, s_q * h_q, 512], ``lse_accum`` fp32 [B + parts, s_q * h_q]
     and, for sparse decode, the gather rows int32 [B, s_q, ceil(topk / 64) * 64].
     """
 
@@ -210,7 +210,7 @@ class DecodeWorkspace:
         rows = s_q * h_q
         self.out = torch.empty((batch, s_q, h_q, D_V), dtype=torch.bfloat16, device=device)
         self.lse = torch.empty((batch, h_q, s_q), dtype=torch.float32, device=device)
-        self.o_accum = torch.empty((batch + num_parts, rows, D_V), dtype=torch.float32,
+        self.o_accum = torch.empty((batch + num_parts, rows, D_V), dtype=torch.bfloat16,
                                    device=device)
         self.lse_accum = torch.empty((batch + num_parts, rows), dtype=torch.float32,
                                      device=device)

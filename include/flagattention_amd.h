@@ -114,9 +114,11 @@ typedef struct fa_mla_decode_args {
    *          lse fp32 [batch][h_q][s_q] contiguous */
   void* out;
   float* lse;
-  /* split workspace: o_accum fp32 [batch+num_parts][s_q*h_q][512],
+  /* split workspace: o_accum bf16 [batch+num_parts][s_q*h_q][512] (each
+   *                  split's normalised output; bf16 halves the traffic of
+   *                  the decode epilogue and of the combine),
    *                  lse_accum fp32 [batch+num_parts][s_q*h_q] */
-  float* o_accum;
+  void* o_accum;
   float* lse_accum;
   int32_t batch, s_q, h_q;
   float softmax_scale;
