@@ -5,10 +5,10 @@
 // possibly spanning several sequences).  All 128 rows share one stream of KV
 // tiles, so every tile enters the CU once.
 //
-// The part is processed as 32-token tiles through a 4-buffer LDS ring: tile
-// t+3 is requested (HBM -> LDS, no VGPR staging) when the computation of tile
-// t starts, so three tiles are in flight per CU.  Each tile goes through two
-// phases separated by work-group barriers:
+// The part is processed as 32-token tiles through a 3-buffer LDS ring: tile
+// t+2 is requested (HBM -> LDS, no VGPR staging) while tile t is multiplied,
+// so two tiles are in flight per CU behind the one being computed.  Each
+// tile goes through two phases separated by work-group barriers:
 //   1. S = Q K^T and the softmax, split by rows: wave w owns rows 32w..32w+31
 //      (its Q^T operand, 32 rows x 576 dims, stays in VGPRs), computes their
 //      S on MFMA 16x16x32 bf16 in four independent accumulator chains and
@@ -30,7 +30,7 @@
 // sequence is processed again with mref preset to the row max found.
 //
 // Unsplit sequences are normalised and written as bf16 out / fp32 lse; split
-// ones write fp32 (o, lse) partials for fa_mla_combine.
+// ones write (o bf16, lse fp32) partials for fa_mla_combine.
 //
 // LDS tile layout: the 32 x 72 grid of 16-byte chunks (row r, logical chunk
 // k) is stored as 4 row-groups x 9 chunk-groups of 1 KB blocks.  Block
@@ -156,6 +156,14 @@ __device__ inline void wait_vmem() {
 // Wave index as a scalar (the compiler cannot tell that threadIdx.x / 64 is
 // uniform across a wave; LDS addresses derived from it must be scalars).
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+// Lane index computed afresh where it is used: volatile asm is neither
+// hoisted nor merged with an earlier copy, so the values derived from it are
+// rebuilt in place instead of being kept (and spilled) across the kernel.
+__device__ inline int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 
 // LDS transpose read (ds_read_b64_tr_b16).  Within each 16-lane group, result
 // lane i, element e comes from source lane 4e + i/4, element i%4: four lanes
@@ -316,13 +324,15 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #define FA_KVBUF(i) ((i) == 0 ? kv_buf0 : (i) == 1 ? kv_buf1 : kv_buf2)
 
   // XCD-aware work-group -> (part, m-block): work-groups are dealt round-robin
-  // over the 8 XCDs, so the m-blocks of one part share an XCD (and its L2).
+  // over the 8 XCDs, and XCD x gets parts x*P/8 .. (x+1)*P/8 - 1 with all
+  // their m-blocks.  Neighbouring parts mostly cut the same sequence, so its
+  // Q rows are fetched into one XCD's L2 instead of several.
   const int wg = blockIdx.x;
   int part, mb;
   if ((a.num_parts & 7) == 0) {
     const int x = wg & 7, k = wg >> 3;
     mb = k % num_m_blocks;
-    part = (k / num_m_blocks) * 8 + x;
+    part = x * (a.num_parts >> 3) + k / num_m_blocks;
   } else {
     part = wg / num_m_blocks;
     mb = wg - part * num_m_blocks;
@@ -354,8 +364,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     if constexpr (kMode == kDense) {
       const int grow = mb * kRows + rho;
       const bool ok = grow < rows_total;
-      s = ok ? grow / a.h_q : 0;
-      hh = ok ? grow - s * a.h_q : 0;
+      // h_q laundered: the division's reciprocal is rebuilt here rather than
+      // kept (and spilled) from the kernel start
+      int hq = a.h_q;
+      asm volatile("" : "+s"(hq));
+      s = ok ? grow / hq : 0;
+      hh = ok ? grow - s * hq : 0;
       return ok;
     } else {
       const int h = hbase + rho;
@@ -365,11 +379,15 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       return ok;
     }
   };
-  // rows this lane computes S and P for: 32*wave + 16rt + i16
-  int own_s[2], own_h[2];
-  bool own_ok[2];
+
+  // query token of the rows this lane computes S and P for (32*wave + 16rt
+  // + i16), for the causal limit
+  int own_s[2];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) own_ok[rt] = map_row(32 * wave + 16 * rt + i16, own_s[rt], own_h[rt]);
+  for (int rt = 0; rt < 2; ++rt) {
+    int hh;
+    map_row(32 * wave + 16 * rt + i16, own_s[rt], hh);
+  }
 
   const float scale_log2 = a.softmax_scale * kLog2e;
   const float ninf = -__builtin_inff();
@@ -470,25 +488,34 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // of each QK, with the first K operands): the VGPRs hold the rest of Q
     // and the pipeline, the AGPRs the O accumulators.  The LDS part goes
     // there directly (LDS-destination loads, 16 bytes per lane = the slot's
-    // lane layout); all of it is waited for only behind the first tile
-    // requests.  Rows past the last one read the zero row.
+    // lane layout).  Issued behind the first two tile requests, so that a
+    // wait for Q does not hold those back.  Rows past the last one read the
+    // zero row.
     bf16x8 qf[kQOps - kQLds];
+    auto load_q = [&]() {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const bf16* qrow =
-          own_ok[rt] ? q + b * a.q_stride_b + own_s[rt] * a.q_stride_s + own_h[rt] * a.q_stride_h + 8 * G
-                     : reinterpret_cast<const bf16*>(g_zero_row);
+      for (int rt = 0; rt < 2; ++rt) {
+        // row indices rebuilt from a fresh lane id: kept from the kernel start
+        // they would be spilled, and their reloads would wait behind the
+        // previous sequence's output stores
+        const int ln = fresh_lane();
+        int s, hh;
+        const bf16* qrow =
+            map_row(32 * wave + 16 * rt + (ln & 15), s, hh)
+                ? q + b * a.q_stride_b + s * a.q_stride_s + hh * a.q_stride_h + 8 * (ln >> 4)
+                : reinterpret_cast<const bf16*>(g_zero_row);
 #pragma unroll
-      for (int kq = 0; kq < kQkSteps; ++kq) {
-        const int j = 2 * kq + rt;
-        if (j >= kQLds) {
-          qf[j - kQLds] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kq);
-        } else {
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(qrow + 32 * kq),
-                                           (FA_LDS void*)(&sm.qx[wave][j][0]), 16, 0, 0);
+        for (int kq = 0; kq < kQkSteps; ++kq) {
+          const int j = 2 * kq + rt;
+          if (j >= kQLds) {
+            qf[j - kQLds] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kq);
+          } else {
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(qrow + 32 * kq),
+                                             (FA_LDS void*)(&sm.qx[wave][j][0]), 16, 0, 0);
+          }
         }
       }
-    }
+    };
     auto q_op = [&](int j) -> bf16x8 {
       return j >= kQLds ? qf[j - kQLds] : sm.qx[wave][j][lane];
     };
@@ -598,21 +625,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
-    float mref_start[2] = {ninf, ninf};
-    for (int pass = 0;; ++pass) {
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        mref[rt] = mref_start[rt];
-        mmax[rt] = ninf;
-        lsum[rt] = 0.f;
-      }
-      overflow = false;
-#pragma unroll
-      for (int dt = 0; dt < kDimTiles; ++dt)
-#pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) acc[dt][rt] = floatx4{};
-
-      // ---- prologue: tiles 0 and 1 requested ----
+    // ---- prologue: tiles 0 and 1 requested (before Q, in the first pass) ----
+    auto prologue = [&]() {
       if constexpr (kMode == kDense) {
         prefetch_page(0);
         copy_all(dense_req(0, kv_buf0, &vq[0]));
@@ -649,6 +663,30 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
         rq0 = load_row(3);
       }
+    };
+    if constexpr (kMode == kSparseFp8) {  // (its prologue waits for everything anyway)
+      load_q();
+      prologue();
+    } else {
+      prologue();
+      load_q();
+    }
+
+    float mref_start[2] = {ninf, ninf};
+    for (int pass = 0;; ++pass) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        mref[rt] = mref_start[rt];
+        mmax[rt] = ninf;
+        lsum[rt] = 0.f;
+      }
+      overflow = false;
+#pragma unroll
+      for (int dt = 0; dt < kDimTiles; ++dt)
+#pragma unroll
+        for (int rt = 0; rt < kRowTiles; ++rt) acc[dt][rt] = floatx4{};
+
+      if (pass > 0) prologue();
 
       // ---- step t: QK(t), softmax(t) -> P | PV(t) ----
       auto step = [&](const int t, auto tag) {
@@ -855,47 +893,56 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     }
     barrier();
     const long long pbase = static_cast<long long>(ns0 + split_local) * rows_total;
+    // lse first: what it needs may have been spilled, and a reload issued
+    // behind the output stores would wait for all of them to complete
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      // the owned rows' (s, head) recomputed from a laundered index: kept
+      // from the kernel start they would be spilled and reloaded here
+      const int ln = fresh_lane();
+      int s, hh;
+      if (map_row(32 * wave + 16 * rt + (ln & 15), s, hh) && ln < 16) {
+        const float lse_v = l_own[rt] > 0.f ? (mref[rt] + log2f(l_own[rt])) * kLn2 : ninf;
+        if (nsplit == 1) {
+          a.lse[(static_cast<long long>(b) * a.h_q + hh) * a.s_q + s] = lse_v;
+        } else if (split_ok) {
+          a.lse_accum[pbase + s * a.h_q + hh] = lse_v;
+        }
+      }
+    }
+    // Row pointers first, stores after: vmcnt counts loads and stores in
+    // order, so a spilled value reloaded between the stores would wait for
+    // every store issued before it.
+    bf16* orow[kRowTiles];
+    float inv[kRowTiles];
 #pragma unroll
     for (int rt = 0; rt < kRowTiles; ++rt) {
       // computed here, per sequence: hoisting these row indices out of the
       // sequence loop would keep 8 of them live through the whole kernel
-      int rho = 16 * rt + i16;
-      asm volatile("" : "+v"(rho));
+      const int ln = fresh_lane();
+      const int rho = 16 * rt + (ln & 15);
       int s, hh;
       const bool ok = map_row(rho, s, hh);
       const float l = reinterpret_cast<const float*>(sm.p)[rho];
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      const int dim0 = 128 * wave + 4 * G;  // + 16 dt + i
-      if (ok && nsplit == 1) {
-        bf16* orow = static_cast<bf16*>(a.out) +
-                     ((static_cast<long long>(b) * a.s_q + s) * a.h_q + hh) * kDv + dim0;
-#pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          uintx2 w;
-          w[0] = pack_bf16x2(acc[dt][rt][0] * inv, acc[dt][rt][1] * inv);
-          w[1] = pack_bf16x2(acc[dt][rt][2] * inv, acc[dt][rt][3] * inv);
-          *reinterpret_cast<uintx2*>(orow + 16 * dt) = w;
-        }
-      } else if (ok && split_ok) {
-        bf16* orow = static_cast<bf16*>(a.o_accum) + (pbase + s * a.h_q + hh) * kDv + dim0;
-#pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          uintx2 w;
-          w[0] = pack_bf16x2(acc[dt][rt][0] * inv, acc[dt][rt][1] * inv);
-          w[1] = pack_bf16x2(acc[dt][rt][2] * inv, acc[dt][rt][3] * inv);
-          *reinterpret_cast<uintx2*>(orow + 16 * dt) = w;
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      inv[rt] = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
+      const int dim0 = 128 * wave + 4 * (ln >> 4);  // + 16 dt + i
+      orow[rt] = !ok ? nullptr
+                 : nsplit == 1
+                     ? static_cast<bf16*>(a.out) +
+                           ((static_cast<long long>(b) * a.s_q + s) * a.h_q + hh) * kDv + dim0
+                 : split_ok ? static_cast<bf16*>(a.o_accum) + (pbase + s * a.h_q + hh) * kDv + dim0
+                            : nullptr;
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      if (own_ok[rt] && G == 0) {
-        const float lse_v = l_own[rt] > 0.f ? (mref[rt] + log2f(l_own[rt])) * kLn2 : ninf;
-        if (nsplit == 1) {
-          a.lse[(static_cast<long long>(b) * a.h_q + own_h[rt]) * a.s_q + own_s[rt]] = lse_v;
-        } else if (split_ok) {
-          a.lse_accum[pbase + own_s[rt] * a.h_q + own_h[rt]] = lse_v;
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+      if (orow[rt] != nullptr) {
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          uintx2 w;
+          w[0] = pack_bf16x2(acc[dt][rt][0] * inv[rt], acc[dt][rt][1] * inv[rt]);
+          w[1] = pack_bf16x2(acc[dt][rt][2] * inv[rt], acc[dt][rt][3] * inv[rt]);
+          *reinterpret_cast<uintx2*>(orow[rt] + 16 * dt) = w;
         }
       }
     }
