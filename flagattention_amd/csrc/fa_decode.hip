@@ -910,41 +910,70 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         }
       }
     }
-    // Row pointers first, stores after: vmcnt counts loads and stores in
-    // order, so a spilled value reloaded between the stores would wait for
-    // every store issued before it.
-    bf16* orow[kRowTiles];
-    float inv[kRowTiles];
+    // Output rows leave through LDS, 32 rows at a time: every wave stages its
+    // 128 dims of the rows (normalised, bf16) in a free tile buffer, then
+    // stores whole 1 KB rows, 16 B per lane, so that a store instruction
+    // writes eight full 128-byte lines rather than sixteen 32-byte pieces.
+    // Staging row r holds 64 16-byte chunks, chunk c at position
+    // c ^ ((r & 7) << 1) (conflict-free 8-byte writes).  Quarter u uses
+    // buffer u % 3; quarter 3's writes come after a barrier that every wave
+    // reaches only once it has read quarter 0.  Row indices and pointers are
+    // rebuilt from a fresh lane id each time: a spilled value reloaded among
+    // the stores would wait for all of them (vmcnt counts in order).
+    if (nsplit == 1 || split_ok) {  // uniform
+      static_for<4>([&](auto qtag) {
+        constexpr int U = decltype(qtag)::value;
+        unsigned char* const stage = FA_KVBUF(U % 3);
+        {
+          const int ln = fresh_lane();
+          const int gq = ln >> 4;
 #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt) {
-      // computed here, per sequence: hoisting these row indices out of the
-      // sequence loop would keep 8 of them live through the whole kernel
-      const int ln = fresh_lane();
-      const int rho = 16 * rt + (ln & 15);
-      int s, hh;
-      const bool ok = map_row(rho, s, hh);
-      const float l = reinterpret_cast<const float*>(sm.p)[rho];
-      inv[rt] = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
-      const int dim0 = 128 * wave + 4 * (ln >> 4);  // + 16 dt + i
-      orow[rt] = !ok ? nullptr
-                 : nsplit == 1
-                     ? static_cast<bf16*>(a.out) +
-                           ((static_cast<long long>(b) * a.s_q + s) * a.h_q + hh) * kDv + dim0
-                 : split_ok ? static_cast<bf16*>(a.o_accum) + (pbase + s * a.h_q + hh) * kDv + dim0
-                            : nullptr;
-    }
-    __builtin_amdgcn_sched_barrier(0);
+          for (int rr = 0; rr < 2; ++rr) {
+            const int rl = 16 * rr + (ln & 15);
+            const float l = reinterpret_cast<const float*>(sm.p)[32 * U + rl];
+            const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
+            unsigned char* const srow = stage + rl * 1024 + 8 * (gq & 1);
+            const int sw = (rl & 7) << 1;
 #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt) {
-      if (orow[rt] != nullptr) {
-#pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          uintx2 w;
-          w[0] = pack_bf16x2(acc[dt][rt][0] * inv[rt], acc[dt][rt][1] * inv[rt]);
-          w[1] = pack_bf16x2(acc[dt][rt][2] * inv[rt], acc[dt][rt][3] * inv[rt]);
-          *reinterpret_cast<uintx2*>(orow[rt] + 16 * dt) = w;
+            for (int dt = 0; dt < kDimTiles; ++dt) {
+              const floatx4 o = acc[dt][2 * U + rr];
+              uintx2 w;
+              w[0] = pack_bf16x2(o[0] * inv, o[1] * inv);
+              w[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
+              *reinterpret_cast<uintx2*>(srow + 16 * ((16 * wave + 2 * dt + (gq >> 1)) ^ sw)) = w;
+            }
+          }
         }
-      }
+        // lane j < 8: the output row of this wave's staging row 8*wave + j
+        unsigned long long rowp;
+        {
+          const int ln = fresh_lane();
+          int s, hh;
+          const bool ok = map_row(32 * U + 8 * wave + (ln & 7), s, hh);
+          const bf16* const p =
+              !ok ? nullptr
+              : nsplit == 1
+                  ? static_cast<bf16*>(a.out) +
+                        ((static_cast<long long>(b) * a.s_q + s) * a.h_q + hh) * kDv
+                  : static_cast<bf16*>(a.o_accum) + (pbase + s * a.h_q + hh) * kDv;
+          rowp = reinterpret_cast<unsigned long long>(p);
+        }
+        barrier();
+        const int ln = fresh_lane();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int rl = 8 * wave + j;  // rl & 7 == j
+          const bf16x8 v =
+              *reinterpret_cast<const bf16x8*>(stage + rl * 1024 + 16 * (ln ^ (j << 1)));
+          const unsigned int lo = __builtin_amdgcn_readlane(static_cast<unsigned int>(rowp), j);
+          const unsigned int hi =
+              __builtin_amdgcn_readlane(static_cast<unsigned int>(rowp >> 32), j);
+          const unsigned long long orow = (static_cast<unsigned long long>(hi) << 32) | lo;
+          if (orow != 0ull) {  // (a global-space pointer: a flat store would also count lgkm)
+            *reinterpret_cast<__attribute__((address_space(1))) bf16x8*>(orow + 16ull * ln) = v;
+          }
+        }
+      });
     }
     barrier();  // LDS (tiles, masks, row sums) is reused by the next sequence
   }
