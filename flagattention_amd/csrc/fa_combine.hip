@@ -10,7 +10,11 @@
 // One 64-lane wave per (sequence, query row); each lane owns 8 of the 512
 // value dims, so a bf16 partial row is one 16-byte load per lane (partials
 // are stored in bf16: the combine and the decode epilogue move half the
-// bytes, and the weighted sum is accumulated in fp32).
+// bytes, and the weighted sum is accumulated in fp32).  The split lse values
+// are loaded one per lane and reduced across the wave, and the partial rows
+// are loaded four at a time, so a row costs three dependent memory round
+// trips whatever its split count (up to 64 splits; more take one extra pass
+// per 64).
 #include "fa_common.h"
 
 namespace fa {
@@ -18,6 +22,18 @@ namespace {
 
 constexpr int kCombineThreads = 256;
 constexpr int kRowsPerBlock = kCombineThreads / 64;
+constexpr int kUnroll = 4;  // partial rows in flight per lane
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
 
 __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
     const bf16* __restrict__ o_accum, const float* __restrict__ lse_accum,
@@ -37,26 +53,57 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
   bf16* orow = out + ((static_cast<long long>(b) * s_q + s) * h_q + h) * kDv + lane * 8;
   float* lse_out = lse + (static_cast<long long>(b) * h_q + h) * s_q + s;
   const float ninf = -__builtin_inff();
+  const float* lrow = lse_accum + static_cast<long long>(s0) * rows + row;  // stride rows
+  const bf16* orows = o_accum + (static_cast<long long>(s0) * rows + row) * kDv + lane * 8;
 
-  float mx = ninf;
-  for (int i = 0; i < ns; ++i)
-    mx = fmaxf(mx, lse_accum[static_cast<long long>(s0 + i) * rows + row]);
+  // lane i holds the lse of split c + i of chunk c (64 splits per chunk)
+  float l0 = lane < ns ? lrow[static_cast<long long>(lane) * rows] : ninf;
+  float mx = l0;
+  for (int c = 64; c < ns; c += 64) {
+    const int i = c + lane;
+    mx = fmaxf(mx, i < ns ? lrow[static_cast<long long>(i) * rows] : ninf);
+  }
+  mx = wave_max(mx);
 
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
   float total = ninf;
   if (mx != ninf) {
-    float sum = 0.f;
-    for (int i = 0; i < ns; ++i)
-      sum += expf(lse_accum[static_cast<long long>(s0 + i) * rows + row] - mx);
-    total = mx + logf(sum);
-    for (int i = 0; i < ns; ++i) {
-      const long long r = static_cast<long long>(s0 + i) * rows + row;
-      const float w = expf(lse_accum[r] - total);
-      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(o_accum + r * kDv + lane * 8);
+    float sum = l0 == ninf ? 0.f : expf(l0 - mx);
+    for (int c = 64; c < ns; c += 64) {
+      const int i = c + lane;
+      const float l = i < ns ? lrow[static_cast<long long>(i) * rows] : ninf;
+      sum += l == ninf ? 0.f : expf(l - mx);
+    }
+    total = mx + logf(wave_sum(sum));
+    for (int c = 0; c < ns; c += 64) {
+      float lc = l0;
+      if (c > 0) {
+        const int i = c + lane;
+        lc = i < ns ? lrow[static_cast<long long>(i) * rows] : ninf;
+      }
+      const float wl = lc == ninf ? 0.f : expf(lc - total);  // weight of split c + lane
+      const int n = min(64, ns - c);
+      for (int j = 0; j < n; j += kUnroll) {
+        // no branches between the loads: past the last split a row is loaded
+        // again and weighs nothing
+        bf16x8 ov[kUnroll];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += w * static_cast<float>(ov[j]);
+        for (int u = 0; u < kUnroll; ++u) {
+          const int jj = min(j + u, n - 1);
+          ov[u] = *reinterpret_cast<const bf16x8*>(orows +
+                                                   static_cast<long long>(c + jj) * rows * kDv);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int jj = min(j + u, n - 1);
+          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), jj));
+          const float w = j + u < n ? wj : 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += w * static_cast<float>(ov[u][e]);
+        }
+      }
     }
   }
   bf16x8 v;

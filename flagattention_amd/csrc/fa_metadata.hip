@@ -5,8 +5,9 @@
 // batch of skewed lengths leaves CUs idle.  Here the work of every sequence
 // (its 64-token blocks plus a fixed per-sequence overhead) is laid end to end
 // in a "cost line" of length W, cut into num_parts equal shares, and each cut
-// is mapped back to a (sequence, block) position.  All steps are prefix sums
-// and binary searches, so one work-group computes it in a few microseconds.
+// is mapped back to a (sequence, block) position.  One work-group, one part
+// per thread: three block scans, two binary searches per part and closed-form
+// divisions for the rest.
 //
 // Spec (integer arithmetic throughout):
 //   nb[b] = ceil(len_b / 64)          (dense; topk > 0: ceil(topk / 64))
@@ -22,160 +23,191 @@
 namespace fa {
 namespace {
 
-constexpr int kMetaThreads = 256;
+constexpr int kMetaThreads = 1024;  // 16 waves: one part per thread (P <= 1024)
+constexpr int kMetaWaves = kMetaThreads / 64;
 constexpr int kMaxB = FA_MLA_MAX_BATCH;
 constexpr int kMaxP = FA_MLA_MAX_PARTS;
+static_assert(kMaxP <= kMetaThreads, "one part per thread");
 
-// Inclusive prefix sum over the work-group (one value per thread): a
-// shuffle scan inside each wave, then the wave totals (two barriers in all;
-// `sh` holds one total per wave and is free again on return).
-__device__ long long block_incl_scan(long long v, long long* sh) {
+// Inclusive prefix sums over the work-group of a 64-bit and a 32-bit value
+// (one pair per thread): a shuffle scan inside each wave, then the wave
+// totals through LDS (two barriers; `sh64` / `sh32` are free again on return).
+__device__ void block_incl_scan2(long long& v, int& k, long long* sh64, int* sh32) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const long long x = __shfl_up(v, off);
-    if (lane >= off) v += x;
+    const int y = __shfl_up(k, off);
+    if (lane >= off) {
+      v += x;
+      k += y;
+    }
   }
-  if (lane == 63) sh[w] = v;
+  if (lane == 63) {
+    sh64[w] = v;
+    sh32[w] = k;
+  }
   __syncthreads();
-  long long base = 0;
-  for (int i = 0; i < w; ++i) base += sh[i];
+  long long bv = 0;
+  int bk = 0;
+  for (int i = 0; i < w; ++i) {
+    bv += sh64[i];
+    bk += sh32[i];
+  }
   __syncthreads();
-  return v + base;
+  v += bv;
+  k += bk;
 }
 
 // Largest i in [0, n) with a[i] <= x (a non-decreasing, a[0] <= x).
 __device__ int last_le(const long long* a, int n, long long x) {
   int lo = 0, hi = n - 1;
   while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
+    const int mid = (lo + hi + 1) >> 1;
     if (a[mid] <= x) lo = mid; else hi = mid - 1;
   }
   return lo;
 }
 
+// floor(a / b) for 0 <= a < 2^53, b > 0: a double-precision estimate, made
+// exact by integer correction (a stays below 2^48 here: P * W with P <= 2^10
+// and W <= 4096 * (2^25 + 4)).
+__device__ inline long long floor_div(long long a, long long b) {
+  long long q = static_cast<long long>(static_cast<double>(a) / static_cast<double>(b));
+  while (q * b > a) --q;
+  while ((q + 1) * b <= a) ++q;
+  return q;
+}
+
 __device__ inline long long seq_blocks(const int32_t* lens, int b, int topk) {
   if (topk > 0) return (topk + kPage - 1) / kPage;
-  int len = lens[b];
+  const int len = lens[b];
   return len > 0 ? (len + kPage - 1) / kPage : 0;
 }
 
 __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     const int32_t* __restrict__ lens, int B, int topk, int P, int overhead,
     int32_t* __restrict__ md, int32_t* __restrict__ num_splits) {
-  __shared__ long long C[kMaxB + 1];
-  __shared__ long long G[kMaxB + 1];
-  __shared__ long long gs[kMaxP + 1];
-  __shared__ int E[kMaxP + 1];
-  __shared__ long long scan_buf[kMetaThreads];
+  __shared__ long long C[kMaxB + 1];  // exclusive prefix of the cost
+  __shared__ long long G[kMaxB + 1];  // exclusive prefix of the blocks
+  __shared__ int pf[kMaxB];           // part holding the first block of sequence b
+  __shared__ int pl[kMaxB];           // part holding its last block
+  __shared__ long long gs[kMaxP + 1];  // first global block of part p
+  __shared__ int owner[kMaxP + 1];     // sequence whose cost interval holds x_p
+  __shared__ int E[kMaxP + 1];         // empty parts in [0, p)
+  __shared__ long long sh64[kMetaWaves];
+  __shared__ int sh32[kMetaWaves];
 
   const int t = threadIdx.x;
+  const int ipt = cdiv(B, kMetaThreads);  // sequences per thread (<= 4)
+  const int b0 = min(B, t * ipt), b1 = min(B, b0 + ipt);
 
-  // 1. cost / block prefix sums over sequences (chunked per thread).
+  // 1. G and the count K of non-empty sequences, scanned together; then
+  //    C[b] = G[b] + overhead * K[b].
   {
-    const int ipt = cdiv(B, kMetaThreads);
-    const int b0 = min(B, t * ipt), b1 = min(B, b0 + ipt);
-    long long csum = 0, gsum = 0;
+    long long gsum = 0;
+    int ksum = 0;
     for (int b = b0; b < b1; ++b) {
-      long long nb = seq_blocks(lens, b, topk);
-      csum += nb > 0 ? nb + overhead : 0;
+      const long long nb = seq_blocks(lens, b, topk);
       gsum += nb;
+      ksum += nb > 0;
     }
-    long long cinc = block_incl_scan(csum, scan_buf);
-    long long ginc = block_incl_scan(gsum, scan_buf);
-    long long cc = cinc - csum, gg = ginc - gsum;
+    long long ginc = gsum;
+    int kinc = ksum;
+    block_incl_scan2(ginc, kinc, sh64, sh32);
+    long long gg = ginc - gsum;
+    long long kk = kinc - ksum;
     for (int b = b0; b < b1; ++b) {
-      long long nb = seq_blocks(lens, b, topk);
-      C[b] = cc;
+      const long long nb = seq_blocks(lens, b, topk);
       G[b] = gg;
-      cc += nb > 0 ? nb + overhead : 0;
+      C[b] = gg + overhead * kk;
       gg += nb;
+      kk += nb > 0;
     }
     if (t == kMetaThreads - 1) {
-      C[B] = cinc;
       G[B] = ginc;
+      C[B] = ginc + static_cast<long long>(overhead) * kinc;
     }
   }
   __syncthreads();
   const long long W = C[B];
   const long long NB = G[B];
 
-  // 2. start of every part on the global block line.
+  // 2. part starts x_p = ceil(p W / P) on the cost line -> global blocks; and
+  //    per sequence, the parts that hold its first and last block, in closed
+  //    form: gs_p <= G[b] exactly when x_p <= C[b] + overhead, and
+  //    gs_p < G[b+1] exactly when x_p < C[b+1], and x_p grows with p.
   for (int p = t; p <= P; p += kMetaThreads) {
-    long long x = (static_cast<long long>(p) * W + P - 1) / P;
+    const long long x = floor_div(static_cast<long long>(p) * W + P - 1, P);
     long long v;
+    int own;
     if (x >= W) {
       v = NB;
+      own = B;
     } else {
-      int b = last_le(C, B, x);
-      long long o = x - C[b] - overhead;
-      v = G[b] + (o > 0 ? o : 0);
+      own = last_le(C, B, x);
+      const long long o = x - C[own] - overhead;
+      v = G[own] + (o > 0 ? o : 0);
     }
     gs[p] = v;
+    owner[p] = own;
+  }
+  for (int b = b0; b < b1; ++b) {
+    if (G[b + 1] > G[b]) {
+      pf[b] = static_cast<int>(floor_div((C[b] + overhead) * P, W));
+      pl[b] = static_cast<int>(floor_div((C[b + 1] - 1) * P, W));
+    }
   }
   __syncthreads();
 
   // 3. E[p] = number of empty parts in [0, p).
   {
-    const int ipt = cdiv(P, kMetaThreads);
-    const int p0 = min(P, t * ipt), p1 = min(P, p0 + ipt);
-    long long cnt = 0;
-    for (int p = p0; p < p1; ++p) cnt += (gs[p] == gs[p + 1]);
-    long long inc = block_incl_scan(cnt, scan_buf);
-    long long e = inc - cnt;
-    for (int p = p0; p < p1; ++p) {
-      E[p] = static_cast<int>(e);
-      e += (gs[p] == gs[p + 1]);
-    }
-    if (t == kMetaThreads - 1) E[P] = static_cast<int>(inc);
+    const int cnt = (t < P && gs[t] == gs[t + 1]) ? 1 : 0;
+    long long unused = 0;
+    int inc = cnt;
+    block_incl_scan2(unused, inc, sh64, sh32);
+    if (t < P) E[t] = inc - cnt;
+    if (t == kMetaThreads - 1) E[P] = inc;
   }
   __syncthreads();
 
-  // 4. per-part descriptors.
-  for (int p = t; p < P; p += kMetaThreads) {
-    const long long g0 = gs[p], g1 = gs[p + 1];
-    int32_t* m = md + static_cast<long long>(p) * kMdStride;
+  // 4. per-part descriptors: a non-empty part starts in the sequence whose
+  //    cost interval holds its x_p.
+  if (t < P) {
+    const long long g0 = gs[t], g1 = gs[t + 1];
+    int4* m = reinterpret_cast<int4*>(md + static_cast<long long>(t) * kMdStride);
     if (g0 == g1) {
-      m[0] = 0; m[1] = 0; m[2] = 0; m[3] = 0;
-      m[4] = 0; m[5] = 0; m[6] = static_cast<int32_t>(g0); m[7] = 0;
-      continue;
+      m[0] = make_int4(0, 0, 0, 0);
+      m[1] = make_int4(0, 0, static_cast<int32_t>(g0), 0);
+    } else {
+      const int bb = owner[t];
+      const int eb = last_le(G, B, g1 - 1);
+      const int f = pf[bb];
+      m[0] = make_int4(bb, static_cast<int32_t>(g0 - G[bb]), eb, static_cast<int32_t>(g1 - G[eb]));
+      m[1] = make_int4((t - f) - (E[t] - E[f]), static_cast<int32_t>(g1 - g0),
+                       static_cast<int32_t>(g0), 0);
     }
-    const int bb = last_le(G, B, g0);
-    const int eb = last_le(G, B, g1 - 1);
-    const int pf = last_le(gs, P, G[bb]);
-    m[0] = bb;
-    m[1] = static_cast<int32_t>(g0 - G[bb]);
-    m[2] = eb;
-    m[3] = static_cast<int32_t>(g1 - G[eb]);
-    m[4] = (p - pf) - (E[p] - E[pf]);
-    m[5] = static_cast<int32_t>(g1 - g0);
-    m[6] = static_cast<int32_t>(g0);
-    m[7] = 0;
   }
 
-  // 5. segments per sequence -> exclusive prefix num_splits[B+1].
+  // 5. segments per sequence (non-empty parts from pf[b] to pl[b]) ->
+  //    exclusive prefix num_splits[B+1].
   {
-    const int ipt = cdiv(B, kMetaThreads);
-    const int b0 = min(B, t * ipt), b1 = min(B, b0 + ipt);
-    long long sum = 0;
+    int segs[4];
+    int sum = 0;
     for (int b = b0; b < b1; ++b) {
-      if (G[b + 1] > G[b]) {
-        int pa = last_le(gs, P, G[b]);
-        int pb = last_le(gs, P, G[b + 1] - 1);
-        sum += (pb - pa + 1) - (E[pb] - E[pa]);
-      }
+      const int n = G[b + 1] > G[b] ? (pl[b] - pf[b] + 1) - (E[pl[b]] - E[pf[b]]) : 0;
+      segs[b - b0] = n;
+      sum += n;
     }
-    long long inc = block_incl_scan(sum, scan_buf);
-    long long acc = inc - sum;
+    long long unused = 0;
+    int inc = sum;
+    block_incl_scan2(unused, inc, sh64, sh32);
+    int acc = inc - sum;
     for (int b = b0; b < b1; ++b) {
-      num_splits[b] = static_cast<int32_t>(acc);
-      if (G[b + 1] > G[b]) {
-        int pa = last_le(gs, P, G[b]);
-        int pb = last_le(gs, P, G[b + 1] - 1);
-        acc += (pb - pa + 1) - (E[pb] - E[pa]);
-      }
+      num_splits[b] = acc;
+      acc += segs[b - b0];
     }
-    if (t == kMetaThreads - 1) num_splits[B] = static_cast<int32_t>(inc);
+    if (t == kMetaThreads - 1) num_splits[B] = inc;
   }
 }
 
@@ -193,6 +225,7 @@ extern "C" int fa_mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, 
   FA_CHECK_ARG(topk >= 0, "topk %d < 0", topk);
   FA_CHECK_ARG(topk > 0 || cache_seqlens != nullptr, "cache_seqlens is NULL");
   FA_CHECK_ARG(tile_md != nullptr && num_splits != nullptr, "output pointer is NULL");
+  FA_CHECK_ARG(reinterpret_cast<uintptr_t>(tile_md) % 16 == 0, "tile_md is not 16-byte aligned");
   hipLaunchKernelGGL(fa::mla_metadata_kernel, dim3(1), dim3(fa::kMetaThreads), 0,
                      static_cast<hipStream_t>(stream), cache_seqlens, batch, topk, num_parts,
                      fixed_overhead, tile_md, num_splits);

@@ -65,10 +65,12 @@ int64_t fa_mla_decode_args_size(void);
  * (blocks + fixed_overhead per sequence) and sequences are cut wherever a
  * share ends.
  *
- *   cache_seqlens  device int32[batch]; ignored when topk > 0
+ *   cache_seqlens  device int32[batch]; ignored when topk > 0.  The total
+ *                  number of 64-token blocks must stay below 2^31 (the
+ *                  descriptors hold global block indices as int32)
  *   topk           > 0: sparse decode, every sequence has ceil(topk/64) blocks
  *   fixed_overhead cost, in blocks, charged per sequence (>= 0)
- *   tile_md        device int32[num_parts][8] (out):
+ *   tile_md        device int32[num_parts][8] (out, 16-byte aligned):
  *                    {begin_batch, begin_block, end_batch, end_block (excl.),
  *                     first_split_local, num_blocks, begin_global_block, 0}
  *   num_splits     device int32[batch+1] (out): exclusive prefix sum of the

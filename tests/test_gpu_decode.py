@@ -38,6 +38,9 @@ def _t(a):
     ([4096 + (i * 977) % 4097 for i in range(64)], 128, 0),
     ([128 * (1 + (i * 7919) % 512) for i in range(32)], 64, 0),
     ([1 + (i * 31) % 100000 for i in range(1000)], 256, 0),
+    # batch / part limits; p * W passes 2^32 (the block total itself stays an int32)
+    ([(i * 2654435761) % 2**25 for i in range(4096)], 1024, 0),
+    ([3000], 1024, 0),
 ])
 def test_metadata_kernel_matches_spec(lens, parts, topk):
     need_gpu()
@@ -135,6 +138,45 @@ def test_dense_bad_page_is_masked_not_faulting():
     kv = orc.gather_rows(kc, good, 0, keep).float()
     ref_o, ref_l = orc.attention_lse(q[0].float().permute(1, 0, 2), kv, kv[:, :512], SCALE, False)
     assert_close(out, lse, ref_o.permute(1, 0, 2).unsqueeze(0), ref_l.unsqueeze(0))
+
+
+
+def _plant_key(kc, bt, b, j, value):
+    """Set logical token j of sequence b to a constant row (all 576 dims)."""
+    kc[int(bt[b, j // 64]), j % 64, 0, :] = value
+
+
+@pytest.mark.parametrize("parts", [None, 3])
+def test_dense_wide_score_spread(parts):
+    """A key scoring > 2^64 above the first tile's row max forces the second pass
+    (the reference is re-based on the row max); the result must still match."""
+    need_gpu()
+    say(f"dense wide score spread parts={parts}")
+    lens = [700, 300]
+    q, kc, bt, ld = orc.make_dense_inputs(2, 128, 1, lens, seed=77, scale=0.1)
+    q.fill_(1.0)
+    # score of the planted key: 576 * 1.5 * 192^-0.5 * log2(e) = 90 (log2 units),
+    # the first tile's scores stay within a few units of 0
+    _plant_key(kc, bt, 0, 500, 1.5)
+    _plant_key(kc, bt, 1, 10, 1.5)  # in the first tile: no second pass needed
+    out, lse, _, _ = run_dense(q, kc, bt, ld, SCALE, False, parts)
+    ref_out, ref_lse = orc.dense_decode_ref(q, kc, bt, ld, SCALE, False)
+    assert float(ref_lse[0].min()) > 60.0  # the planted key dominates
+    assert_close(out, lse, ref_out, ref_lse)
+
+
+def test_sparse_wide_score_spread():
+    need_gpu()
+    say("sparse wide score spread")
+    lens = [3000, 3000]
+    q, kc, bt, ld = orc.make_dense_inputs(2, 128, 1, lens, seed=78, scale=0.1)
+    q.fill_(1.0)
+    idx = orc.make_sparse_indices(2, 1, 1024, lens, seed=79, invalid_frac=0.0)
+    _plant_key(kc, bt, 0, int(idx[0, 0, 900]), 1.5)  # index slot 900: a late tile
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE)
+    ref_out, ref_lse = orc.sparse_decode_ref(q, kc, bt, ld, idx, SCALE)
+    assert float(ref_lse[0].min()) > 60.0
+    assert_close(out, lse, ref_out, ref_lse)
 
 
 # ---------------------------------------------------------------- sparse
