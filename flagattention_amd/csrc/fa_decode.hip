@@ -259,42 +259,45 @@ __device__ inline unsigned int pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(unsigned int, __builtin_convertvector(f, bf16x2));  // one v_cvt_pk_bf16_f32
 }
 
-// Raw fp8 row slice held by one thread: (tile row r, eighth p) -> 64 latent
-// codes (dims 64p..64p+63), their fp32 scale and 8 rope dims.
-struct Fp8Slice {
+// fp8 tiles reach LDS raw, one row-group (8 tile rows) per wave, inside the
+// row-group's own 9 KB of the bf16 tile buffer:
+//   [0, 4096)      codes: block G (1 KB) holds codes 128G..128G+127 of the 8
+//                  rows, slot 8r + c = row r, 16-byte chunk c
+//   [4096, 5120)   the four fp32 scales of row r at 4096 + 128r (the copy
+//                  lanes of a row all load them; slot 8r is the one read)
+//   [8192, 9216)   the rope dims, already in the bf16 layout (chunk-group 8)
+// and the wave that loaded them turns the codes into bf16 blocks 0..7 in
+// place.  Those overlap the raw bytes, so every read of the row-group comes
+// before its first write; no other wave touches the row-group meanwhile.
+constexpr int kFp8Copies = 6;          // wave-wide 16-byte copies per row-group
+constexpr int kFp8ScaleOff = 4096;
+
+__device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
+  // addresses rebuilt from a fresh lane id: kept live across the loop they
+  // would be spilled, and each reload would stall the conversion
+  const int lane = fresh_lane();
+  const int r = lane >> 3, e = lane & 7;  // row r of the group, codes 64e..64e+63
+  const unsigned char* rg = buf + wave * kRowGroupBytes;
+  const unsigned char* src = rg + 1024 * (e >> 1) + 16 * (8 * r + 4 * (e & 1));
   uintx4 code[4];
-  float scale;
-  uintx4 rope;
-};
-
-// `row` points at a cache row, or at g_zero_row for a masked slot (all
-// codes, the scale and the rope dims then read as zero).
-__device__ inline void load_fp8_slice(Fp8Slice& f, const unsigned char* row, int p) {
-  const uintx4* c = reinterpret_cast<const uintx4*>(row + 64 * p);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f.code[i] = c[i];
-  f.scale = *reinterpret_cast<const float*>(row + 512 + 4 * (p >> 1));
-  f.rope = *reinterpret_cast<const uintx4*>(row + 528 + 16 * p);
-}
-
-// Dequantise into the bf16 tile: logical chunks 8p..8p+7 and rope chunk 64+p.
-__device__ inline void store_fp8_slice(unsigned char* buf, const Fp8Slice& f, int r, int p) {
+  for (int i = 0; i < 4; ++i) code[i] = *reinterpret_cast<const uintx4*>(src + 16 * i);
+  const float scale = *reinterpret_cast<const float*>(rg + kFp8ScaleOff + 128 * r + 4 * (e >> 1));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {  // 8 codes -> 8 bf16 = one 16-byte chunk
-      const unsigned int w0 = f.code[i][2 * h], w1 = f.code[i][2 * h + 1];
+      const unsigned int w0 = code[i][2 * h], w1 = code[i][2 * h + 1];
       floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
       floatx2 c = fp8x2_to_f32<false>(w1), d = fp8x2_to_f32<true>(w1);
       uintx4 o;
-      o[0] = pack_bf16x2(a[0] * f.scale, a[1] * f.scale);
-      o[1] = pack_bf16x2(b[0] * f.scale, b[1] * f.scale);
-      o[2] = pack_bf16x2(c[0] * f.scale, c[1] * f.scale);
-      o[3] = pack_bf16x2(d[0] * f.scale, d[1] * f.scale);
-      *reinterpret_cast<uintx4*>(buf + tile_off(r, 8 * p + 2 * i + h)) = o;
+      o[0] = pack_bf16x2(a[0] * scale, a[1] * scale);
+      o[1] = pack_bf16x2(b[0] * scale, b[1] * scale);
+      o[2] = pack_bf16x2(c[0] * scale, c[1] * scale);
+      o[3] = pack_bf16x2(d[0] * scale, d[1] * scale);
+      *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * i + h)) = o;
     }
   }
-  *reinterpret_cast<uintx4*>(buf + tile_off(r, 64 + p)) = f.rope;
 }
 
 template <int V>
@@ -450,7 +453,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     return static_cast<unsigned int>((8 * wave + lr) * static_cast<int>(row_stride) +
                                      16 * ((ln & 7) ^ lr ^ (wave & 1)));
   };
-  const int f8_p = lane & 7;  // fp8: eighth of tile row 8*wave + lrow
 
   // Metadata from another batch / topk must not drive accesses out of bounds:
   // sequence, block and split indices are clamped to this call's shapes.
@@ -521,10 +523,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     };
 
     // ---- tile producers ----
-    // bf16 tiles go HBM -> LDS directly, requested two tiles ahead.  fp8
-    // tiles are loaded into registers three tiles ahead and dequantised into
-    // LDS two tiles ahead.  Every lane issues the same loads for every tile
-    // (masked rows / pages read zeros), so the vmcnt waits are constants.
+    // Tiles go HBM -> LDS directly, requested two tiles ahead (fp8: raw,
+    // converted in place one tile ahead by the wave that loaded each
+    // row-group).  Every lane issues the same loads for every tile (masked
+    // rows / pages read zeros), so the vmcnt waits are constants.
     // dense: page of the next tile to request, looked up one step ahead
     int next_page = -1;
     auto prefetch_page = [&](int u) {
@@ -551,10 +553,29 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       } else if constexpr (kMode == kSparseBf16) {
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(c.src + 128 * Gc),
                                          (FA_LDS void*)(c.dst + Gc * kBlockBytes), 16, 0, 0);
+      } else {
+        // fp8 raw layout (c.src = this lane's row): codes 128Gc + 16(lane%8)
+        // for Gc < 4, the scales, then the rope chunk of the bf16 slot
+        const int l8 = lane & 7;
+        const unsigned char* src;
+        unsigned char* dst;
+        if constexpr (Gc < 4) {
+          src = c.src + 128 * Gc + 16 * l8;
+          dst = c.dst + Gc * kBlockBytes;
+        } else if constexpr (Gc == 4) {
+          src = c.src + 512;
+          dst = c.dst + kFp8ScaleOff;
+        } else {
+          src = c.src + 528 + 16 * (l8 ^ lrow ^ (wave & 1));
+          dst = c.dst + 8 * kBlockBytes;
+        }
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (FA_LDS void*)dst,
+                                         16, 0, 0);
       }
     };
+    constexpr int kCopies = kMode == kSparseFp8 ? kFp8Copies : kCopiesPerWave;
     auto copy_all = [&](const CopyReq& c) {
-      static_for<kChunkGroups>([&](auto gt) { copy_block(c, gt); });
+      static_for<kCopies>([&](auto gt) { copy_block(c, gt); });
     };
     // dense: request of tile u's half page (rows past the sequence, or a page
     // id outside the cache, read as zeros); *mask = its key mask
@@ -594,19 +615,20 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     auto row_mask = [&](int32_t r) -> unsigned int {
       return static_cast<unsigned int>(__ballot(r >= 0));
     };
-    // sparse bf16: gathered rows (r = the rows of lanes 0..31)
+    // sparse: gathered rows (r = the rows of lanes 0..31); bf16: this lane's
+    // chunk of its row, fp8: its row (the copies add their offsets)
     auto gather_req = [&](int32_t r, unsigned char* buf) -> CopyReq {
       CopyReq c;
       c.rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
-      c.src = row_ptr(__shfl(r, 8 * wave + lrow)) + 16 * ((lane & 7) ^ lrow ^ (wave & 1));
+      c.src = row_ptr(__shfl(r, 8 * wave + lrow));
+      if constexpr (kMode == kSparseBf16) c.src += 16 * ((lane & 7) ^ lrow ^ (wave & 1));
       c.voff = 0;
       c.dst = buf + wave * kRowGroupBytes;
       return c;
     };
-    int32_t rq0 = -1, rq1 = -1;  // sparse: rows of tiles t+2 and t+3 (fp8: t+3)
-    // key masks of tiles t.. (scalar queue; bit j: token j of the tile)
-    unsigned int vq[3] = {0u, 0u, 0u};
-    Fp8Slice f8;
+    int32_t rq0 = -1, rq1 = -1;  // sparse: rows of tiles t+2 and t+3
+    // key masks of tiles t, t+1 (scalar queue; bit j: token j of the tile)
+    unsigned int vq[2] = {0u, 0u};
 
     // ---- softmax state of the two owned rows (log2 units) ----
     constexpr float kHeadroom = 64.f;
@@ -633,7 +655,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         prefetch_page(1);
         copy_all(dense_req(1, kv_buf1, &vq[1]));
         prefetch_page(2);
-      } else if constexpr (kMode == kSparseBf16) {
+      } else {
         const int32_t r0l = load_row(0), r1l = load_row(1);
         wait_vmem<0>();
         const int32_t r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
@@ -645,32 +667,18 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         rq0 = load_row(2);
         copy_all(gather_req(r1, kv_buf1));
         rq1 = load_row(3);
-      } else {
-        int32_t r = load_row(0);
-        wait_vmem<0>();
-        r = row_valid(0, r);
-        vq[0] = row_mask(r);
-        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
-        r = row_valid(1, load_row(1));
-        wait_vmem<0>();
-        store_fp8_slice(kv_buf0, f8, 8 * wave + lrow, f8_p);
-        vq[1] = row_mask(r);
-        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
-        r = row_valid(2, load_row(2));
-        wait_vmem<0>();
-        store_fp8_slice(kv_buf1, f8, 8 * wave + lrow, f8_p);
-        vq[2] = row_mask(r);
-        load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
-        rq0 = load_row(3);
       }
     };
-    if constexpr (kMode == kSparseFp8) {  // (its prologue waits for everything anyway)
-      load_q();
-      prologue();
-    } else {
-      prologue();
-      load_q();
-    }
+    // fp8: tile 0 is converted once its raw copies landed (tile t+1 by step t)
+    auto fp8_first_tile = [&]() {
+      if constexpr (kMode == kSparseFp8) {
+        wait_vmem<0>();
+        dequant_fp8_rowgroup(kv_buf0, wave);
+      }
+    };
+    prologue();
+    load_q();
+    fp8_first_tile();
 
     float mref_start[2] = {ninf, ninf};
     for (int pass = 0;; ++pass) {
@@ -686,16 +694,19 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #pragma unroll
         for (int rt = 0; rt < kRowTiles; ++rt) acc[dt][rt] = floatx4{};
 
-      if (pass > 0) prologue();
+      if (pass > 0) {
+        prologue();
+        fp8_first_tile();
+      }
 
       // ---- step t: QK(t), softmax(t) -> P | PV(t) ----
       auto step = [&](const int t, auto tag) {
         constexpr int K = decltype(tag)::value;  // t % 3
         unsigned char* const b_cur = FA_KVBUF(K);
         unsigned char* const b_cp = FA_KVBUF((K + 2) % 3);
-        // this wave's copies of tile t landed (those of t+1 may be in flight),
-        // then everyone's; everyone is done with step t-1, which frees buffer
-        // (t+2) % 3
+        // this wave's copies of tile t landed (those of t+1 may be in flight;
+        // fp8: those of t+1 too, converted below), then everyone's; everyone
+        // is done with step t-1, which frees buffer (t+2) % 3
         if constexpr (kMode == kSparseFp8) {
           wait_vmem<0>();
         } else if constexpr (kMode == kSparseBf16) {
@@ -720,13 +731,15 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           vq[0] = vq[1];
           vq[1] = row_mask(r);
         } else {
-          store_fp8_slice(b_cp, f8, 8 * wave + lrow, f8_p);
-          const int32_t r = row_valid(t + 3, rq0);
-          load_fp8_slice(f8, row_ptr(__shfl(r, 8 * wave + lrow)), f8_p);
-          rq0 = load_row(t + 4);
+          // fp8: this wave's row-group of tile t+1 (its raw copies landed
+          // with the wait above) becomes bf16; it is read from step t+1 on
+          dequant_fp8_rowgroup(FA_KVBUF((K + 1) % 3), wave);
+          const int32_t r = row_valid(t + 2, rq0);
+          rq0 = rq1;
+          rq1 = load_row(t + 4);
+          creq = gather_req(r, b_cp);
           vq[0] = vq[1];
-          vq[1] = vq[2];
-          vq[2] = row_mask(r);
+          vq[1] = row_mask(r);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -750,7 +763,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
               ka[(kq + kPre) % kRing][1] = k_read(lo, b_cur, kq + kPre, 1);
             }
             const bf16x8 q0 = q_op(2 * kq), q1 = q_op(2 * kq + 1);
-            if constexpr (kMode != kSparseFp8 && (kq & 1) == 0 && (kq >> 1) < kChunkGroups)
+            if constexpr ((kq & 1) == 0 && (kq >> 1) < kCopies)
               copy_block(creq, IntTag<(kq >> 1)>{});
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 a0 = ka[kq % kRing][0], a1 = ka[kq % kRing][1];
