@@ -6,7 +6,9 @@ A step is one decode of the whole batch through the public path: scheduler metad
 (get_mla_metadata) + decode + split combine, with every input already resident in HBM.
 The default workload is BASELINE config 2 (dense bf16, B=64, h_q=128, s_q=1, lengths
 U[4096, 8192], 64-token pages through a permuted block table).  KV pools are rotated
-between steps so consecutive steps do not hit the 256 MB last-level cache.
+between steps so consecutive steps do not hit the 256 MB last-level cache.  The default
+500 warm-up steps (about 0.1 s of GPU work) bring the GPU to its steady clocks: after only
+10, the decode kernel still runs about 20% slower.
 
 Prints one JSON line: value = wall-clock us/step (lower is better); `roofline` is the
 decode kernel alone (HIP events around its launch on the launch stream), algorithmic
@@ -200,8 +202,8 @@ def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--workload", default="dense",
                     choices=["dense", "skew", "sparse", "sparse_fp8"])
     ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
