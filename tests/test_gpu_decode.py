@@ -209,6 +209,36 @@ def test_sparse_random(fp8, topk, parts):
     assert_close(out, lse, ref_out, ref_lse)
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("h_q,s_q,topk", [(100, 2, 300), (256, 1, 500), (16, 3, 64)])
+def test_sparse_head_and_token_shapes(fp8, h_q, s_q, topk):
+    """Head counts that are not a multiple of the 128-row work-group, several query
+    tokens (each with its own top-k), and more than one head block per token."""
+    need_gpu()
+    say(f"sparse shapes fp8={fp8} h_q={h_q} s_q={s_q} topk={topk}")
+    lens = [700, 1500]
+    q, kc, bt, ld = orc.make_dense_inputs(2, h_q, s_q, lens, seed=h_q + topk, scale=0.1,
+                                          extra_blocks=1)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=topk + 7)
+    idx = orc.make_sparse_indices(2, s_q, topk, lens, seed=topk + 3)
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8)
+    ref_out, ref_lse = orc.sparse_decode_ref(q, kc, bt, ld, idx, SCALE, is_fp8=fp8)
+    assert_close(out, lse, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("h_q,s_q,causal", [(256, 1, False), (128, 2, True), (64, 5, True)])
+def test_dense_multi_row_block(h_q, s_q, causal):
+    """More than 128 query rows per sequence: several row blocks per part."""
+    need_gpu()
+    say(f"dense row blocks h_q={h_q} s_q={s_q} causal={causal}")
+    lens = [1000, 3000, 65]
+    q, kc, bt, ld = orc.make_dense_inputs(3, h_q, s_q, lens, seed=h_q * s_q, scale=0.5)
+    out, lse, _, _ = run_dense(q, kc, bt, ld, SCALE, causal)
+    ref_out, ref_lse = orc.dense_decode_ref(q, kc, bt, ld, SCALE, causal)
+    assert_close(out, lse, ref_out, ref_lse)
+
+
 def test_sparse_all_masked_row():
     need_gpu()
     q, kc, bt, ld = orc.make_dense_inputs(2, 64, 1, [300, 300], seed=4)
