@@ -783,10 +783,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           mfma_vacc_drain(sacc);
         }
 
-        // V^T operands of PV(t), read now so that the softmax hides them
+        // V^T operands of PV(t), read now so that the softmax hides them (as
+        // many as the registers allow: all of them for dense decode)
+        constexpr int kVPre = kMode == kDense ? kDimTiles : 4;
         bf16x8 va[kDimTiles];
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) va[dt] = v_read(lo, b_cur, dt);
+        for (int dt = 0; dt < kVPre; ++dt) va[dt] = v_read(lo, b_cur, dt);
         __builtin_amdgcn_sched_barrier(0);
 
         // softmax(t) of the owned rows: row 32*wave + 16rt + i16, tokens
@@ -844,7 +846,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         // tiles ahead
         {
 #pragma unroll
-          for (int dt = 2; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
+          for (int dt = kVPre; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
           bf16x8 pb[2];
           auto p_read = [&](int rt) -> bf16x8 {
             return *reinterpret_cast<const bf16x8*>(sm.p + lo.pr + rt * 1024);
