@@ -40,9 +40,23 @@ MD_STRIDE = 8
 FP8_ROW_BYTES = 656
 MAX_BATCH = 4096
 MAX_PARTS = 1024
-# Scheduler cost, in 64-token blocks, charged once per sequence segment
-# (Q load, partial write-out and its share of the combine).
+# Scheduler cost, in 64-token blocks, charged once per sequence on the cost line
+# (a sequence start inside a part adds a segment there: Q load, partial write-out and
+# its share of the combine).
 FIXED_OVERHEAD_BLOCKS = 4
+
+
+def overhead_blocks(sparse: bool) -> int:
+    """Per-sequence scheduler overhead for dense / sparse decode.
+
+    Every part pays for its first segment whatever it holds, so the overhead only
+    balances parts that hold a second one.  Sparse sequences all have ceil(topk / 64)
+    blocks, and with the default part count (a multiple of the batch for the usual
+    shapes) the cuts fall on sequence starts: charging the overhead there would shrink
+    the first part of every sequence instead (18 vs 10 tiles per part at B = 64,
+    topk = 2048, P = 256), so sparse decode charges none.
+    """
+    return 0 if sparse else FIXED_OVERHEAD_BLOCKS
 
 
 class MLAArgumentError(ValueError, AssertionError):
@@ -133,7 +147,8 @@ def get_mla_metadata(
     lib = _lib.load()
     with torch.cuda.device(device):
         _lib.check(lib.fa_mla_get_metadata(
-            _ptr(cache_seqlens), batch, int(topk or 0), num_sm_parts, FIXED_OVERHEAD_BLOCKS,
+            _ptr(cache_seqlens), batch, int(topk or 0), num_sm_parts,
+            overhead_blocks(topk is not None),
             _ptr(tile_md), _ptr(num_splits), _stream(device)))
     return tile_md, num_splits
 

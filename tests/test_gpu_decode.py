@@ -48,7 +48,7 @@ def test_metadata_kernel_matches_spec(lens, parts, topk):
     ld = torch.tensor(lens, dtype=torch.int32, device=DEV)
     md, ns = fa.get_mla_metadata(ld, 128, 1, topk=topk or None, num_sm_parts=parts)
     torch.cuda.synchronize()
-    want_md, want_ns = orc.metadata_spec(lens, parts, fa.mla.FIXED_OVERHEAD_BLOCKS, topk)
+    want_md, want_ns = orc.metadata_spec(lens, parts, fa.mla.overhead_blocks(bool(topk)), topk)
     assert md.cpu().tolist() == want_md
     assert ns.cpu().tolist() == want_ns
 
