@@ -116,13 +116,16 @@ def build_inputs(spec, dev, copies):
 
 
 def algorithmic_work(spec, lens_cpu, indices) -> tuple:
-    """HBM bytes and FLOPs one decode launch must move / compute."""
+    """HBM bytes and FLOPs one decode launch must move / compute: every KV row it
+    attends to once, q in, out (or the split partial) and lse out, and the block-table
+    words (dense) or translated row ids (sparse) that address the rows; FLOPs of QK (576)
+    and PV (512) per row and head."""
     b, s_q, h_q = spec["batch"], spec["s_q"], spec["h_q"]
     row_bytes = 656 if spec["fp8"] else 1152
     if spec["topk"]:
         n_valid = int((indices >= 0).sum())  # per (b, s) token lists
         kv_rows = n_valid
-        table = indices.numel() * 4
+        table = indices.numel() * 4  # the translated row ids
         flops_rows = n_valid  # each valid (b, s, token) pair meets h_q heads once
     else:
         kv_rows = int(lens_cpu.sum())
