@@ -127,6 +127,18 @@ def test_dense_split_invariance():
     assert torch.allclose(l1, l2, atol=1e-4)
 
 
+def test_dense_many_splits_vs_oracle():
+    """A sequence cut into more than 64 splits (the combine reduces split weights in
+    chunks of 64 lanes) against the oracle."""
+    need_gpu()
+    lens = [20000, 700]
+    q, kc, bt, ld = orc.make_dense_inputs(2, 16, 1, lens, seed=31, scale=0.5)
+    out, lse, _, ns = run_dense(q, kc, bt, ld, SCALE, False, 512)
+    assert int(ns[1] - ns[0]) > 128
+    ref_out, ref_lse = orc.dense_decode_ref(q, kc, bt, ld, SCALE, False)
+    assert_close(out, lse, ref_out, ref_lse)
+
+
 def test_dense_bad_page_is_masked_not_faulting():
     """A block-table entry outside the cache reads as a masked page."""
     need_gpu()
