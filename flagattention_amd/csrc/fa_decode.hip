@@ -800,14 +800,42 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 
         // softmax(t) of the owned rows: row 32*wave + 16rt + i16, tokens
         // 16tt + 4G + i (8 per row and lane)
+        const bool partial = vm != ~0u || t >= causal_from;  // uniform
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           float sv[8];
+          // dense, full tile, reference set (uniform; the usual case): scores
+          // relative to the reference in one fma each; the running max is
+          // kept absolute (the reference plus the relative max).  (Sparse
+          // tiles are partial about half the time, where the test costs more
+          // than it saves.)
+          if (kMode == kDense && !partial && __ballot(mref[rt] == ninf) == 0ull) {
+            const float nmu = -mref[rt];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                sv[4 * tt + i] = __builtin_fmaf(sacc[tt][rt][i], scale_log2, nmu);
+            const float mr = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+            mmax[rt] = fmaxf(mmax[rt], mr + mref[rt]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sv[i] = __builtin_amdgcn_exp2f(sv[i]);
+            lsum[rt] += ((sv[0] + sv[1]) + (sv[2] + sv[3])) + ((sv[4] + sv[5]) + (sv[6] + sv[7]));
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+              uintx2 w;
+              w[0] = pack_bf16x2(sv[4 * tt + 0], sv[4 * tt + 1]);
+              w[1] = pack_bf16x2(sv[4 * tt + 2], sv[4 * tt + 3]);
+              *reinterpret_cast<uintx2*>(sm.p + lo.pw[tt] + rt * 1024) = w;
+            }
+            continue;
+          }
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) sv[4 * tt + i] = sacc[tt][rt][i] * scale_log2;
-          if (vm != ~0u || t >= causal_from) {  // partial tile (uniform branch)
+          if (partial) {
             const unsigned int vmg = vm >> (4 * G);
             const int lim = row_limit(rt) - kTileRows * t - 4 * G;
 #pragma unroll
