@@ -56,8 +56,17 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
   const float* lrow = lse_accum + static_cast<long long>(s0) * rows + row;  // stride rows
   const bf16* orows = o_accum + (static_cast<long long>(s0) * rows + row) * kDv + lane * 8;
 
-  // lane i holds the lse of split c + i of chunk c (64 splits per chunk)
+  // lane i holds the lse of split c + i of chunk c (64 splits per chunk).
+  // The first kUnroll partial rows do not depend on the lse: they are loaded
+  // beside it, so the wave waits for memory twice rather than three times.
   float l0 = lane < ns ? lrow[static_cast<long long>(lane) * rows] : ninf;
+  bf16x8 ov0[kUnroll] = {};
+  if (ns > 0) {  // uniform; a sequence without keys has no partial rows
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      ov0[u] = *reinterpret_cast<const bf16x8*>(
+          orows + static_cast<long long>(min(u, ns - 1)) * rows * kDv);
+  }
   float mx = l0;
   for (int c = 64; c < ns; c += 64) {
     const int i = c + lane;
@@ -77,6 +86,18 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
       sum += l == ninf ? 0.f : expf(l - mx);
     }
     total = mx + logf(wave_sum(sum));
+    // acc += weight(split c + j + u) * row, u < kUnroll; rows past the
+    // chunk's last split are repeats of it and weigh nothing
+    auto accumulate = [&](const bf16x8* ov, float wl, int j, int n) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int jj = min(j + u, n - 1);
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), jj));
+        const float w = j + u < n ? wj : 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w * static_cast<float>(ov[u][e]);
+      }
+    };
     for (int c = 0; c < ns; c += 64) {
       float lc = l0;
       if (c > 0) {
@@ -85,7 +106,12 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
       }
       const float wl = lc == ninf ? 0.f : expf(lc - total);  // weight of split c + lane
       const int n = min(64, ns - c);
-      for (int j = 0; j < n; j += kUnroll) {
+      int j = 0;
+      if (c == 0) {
+        accumulate(ov0, wl, 0, n);
+        j = kUnroll;
+      }
+      for (; j < n; j += kUnroll) {
         // no branches between the loads: past the last split a row is loaded
         // again and weighs nothing
         bf16x8 ov[kUnroll];
@@ -95,14 +121,7 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
           ov[u] = *reinterpret_cast<const bf16x8*>(orows +
                                                    static_cast<long long>(c + jj) * rows * kDv);
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int jj = min(j + u, n - 1);
-          const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), jj));
-          const float w = j + u < n ? wj : 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += w * static_cast<float>(ov[u][e]);
-        }
+        accumulate(ov, wl, j, n);
       }
     }
   }

@@ -23,15 +23,19 @@
 namespace fa {
 namespace {
 
-constexpr int kMetaThreads = 1024;  // 16 waves: one part per thread (P <= 1024)
-constexpr int kMetaWaves = kMetaThreads / 64;
+// One part per thread (P <= threads) and at most four sequences per thread
+// (B <= 4 * threads): 1024 threads cover every valid call, and 256 threads
+// (fewer waves in every scan) the calls with P <= 256 and B <= 1024.
+constexpr int kMetaThreadsMax = 1024;
+constexpr int kMetaThreadsSmall = 256;
 constexpr int kMaxB = FA_MLA_MAX_BATCH;
 constexpr int kMaxP = FA_MLA_MAX_PARTS;
-static_assert(kMaxP <= kMetaThreads, "one part per thread");
+static_assert(kMaxP <= kMetaThreadsMax && kMaxB <= 4 * kMetaThreadsMax, "one block covers a call");
 
 // Inclusive prefix sums over the work-group of a 64-bit and a 32-bit value
 // (one pair per thread): a shuffle scan inside each wave, then the wave
 // totals through LDS (two barriers; `sh64` / `sh32` are free again on return).
+template <int kWaves>
 __device__ void block_incl_scan2(long long& v, int& k, long long* sh64, int* sh32) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -48,12 +52,17 @@ __device__ void block_incl_scan2(long long& v, int& k, long long* sh64, int* sh3
     sh32[w] = k;
   }
   __syncthreads();
-  long long bv = 0;
-  int bk = 0;
-  for (int i = 0; i < w; ++i) {
-    bv += sh64[i];
-    bk += sh32[i];
+  // the totals of the waves before this one: lane i < w reads wave i's, and a
+  // sum over lanes 0..15 (xor partners within the group) adds them up
+  long long bv = lane < w ? sh64[lane] : 0;
+  int bk = lane < w ? sh32[lane] : 0;
+#pragma unroll
+  for (int off = 1; off < kWaves; off <<= 1) {
+    bv += __shfl_xor(bv, off);
+    bk += __shfl_xor(bk, off);
   }
+  bv = __shfl(bv, 0);
+  bk = __shfl(bk, 0);
   __syncthreads();
   v += bv;
   k += bk;
@@ -85,6 +94,7 @@ __device__ inline long long seq_blocks(const int32_t* lens, int b, int topk) {
   return len > 0 ? (len + kPage - 1) / kPage : 0;
 }
 
+template <int kMetaThreads>
 __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     const int32_t* __restrict__ lens, int B, int topk, int P, int overhead,
     int32_t* __restrict__ md, int32_t* __restrict__ num_splits) {
@@ -95,6 +105,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   __shared__ long long gs[kMaxP + 1];  // first global block of part p
   __shared__ int owner[kMaxP + 1];     // sequence whose cost interval holds x_p
   __shared__ int E[kMaxP + 1];         // empty parts in [0, p)
+  constexpr int kMetaWaves = kMetaThreads / 64;
   __shared__ long long sh64[kMetaWaves];
   __shared__ int sh32[kMetaWaves];
 
@@ -114,7 +125,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     }
     long long ginc = gsum;
     int kinc = ksum;
-    block_incl_scan2(ginc, kinc, sh64, sh32);
+    block_incl_scan2<kMetaWaves>(ginc, kinc, sh64, sh32);
     long long gg = ginc - gsum;
     long long kk = kinc - ksum;
     for (int b = b0; b < b1; ++b) {
@@ -165,7 +176,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     const int cnt = (t < P && gs[t] == gs[t + 1]) ? 1 : 0;
     long long unused = 0;
     int inc = cnt;
-    block_incl_scan2(unused, inc, sh64, sh32);
+    block_incl_scan2<kMetaWaves>(unused, inc, sh64, sh32);
     if (t < P) E[t] = inc - cnt;
     if (t == kMetaThreads - 1) E[P] = inc;
   }
@@ -201,7 +212,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     }
     long long unused = 0;
     int inc = sum;
-    block_incl_scan2(unused, inc, sh64, sh32);
+    block_incl_scan2<kMetaWaves>(unused, inc, sh64, sh32);
     int acc = inc - sum;
     for (int b = b0; b < b1; ++b) {
       num_splits[b] = acc;
@@ -226,9 +237,16 @@ extern "C" int fa_mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, 
   FA_CHECK_ARG(topk > 0 || cache_seqlens != nullptr, "cache_seqlens is NULL");
   FA_CHECK_ARG(tile_md != nullptr && num_splits != nullptr, "output pointer is NULL");
   FA_CHECK_ARG(reinterpret_cast<uintptr_t>(tile_md) % 16 == 0, "tile_md is not 16-byte aligned");
-  hipLaunchKernelGGL(fa::mla_metadata_kernel, dim3(1), dim3(fa::kMetaThreads), 0,
-                     static_cast<hipStream_t>(stream), cache_seqlens, batch, topk, num_parts,
-                     fixed_overhead, tile_md, num_splits);
+  const bool small = num_parts <= fa::kMetaThreadsSmall && batch <= 4 * fa::kMetaThreadsSmall;
+  if (small) {
+    hipLaunchKernelGGL(fa::mla_metadata_kernel<fa::kMetaThreadsSmall>, dim3(1),
+                       dim3(fa::kMetaThreadsSmall), 0, static_cast<hipStream_t>(stream),
+                       cache_seqlens, batch, topk, num_parts, fixed_overhead, tile_md, num_splits);
+  } else {
+    hipLaunchKernelGGL(fa::mla_metadata_kernel<fa::kMetaThreadsMax>, dim3(1),
+                       dim3(fa::kMetaThreadsMax), 0, static_cast<hipStream_t>(stream),
+                       cache_seqlens, batch, topk, num_parts, fixed_overhead, tile_md, num_splits);
+  }
   FA_CHECK_HIP(hipGetLastError());
   return FA_OK;
 }

@@ -38,6 +38,10 @@ def _t(a):
     ([4096 + (i * 977) % 4097 for i in range(64)], 128, 0),
     ([128 * (1 + (i * 7919) % 512) for i in range(32)], 64, 0),
     ([1 + (i * 31) % 100000 for i in range(1000)], 256, 0),
+    # either side of the 256-thread launch's limits (P <= 256, B <= 1024)
+    ([1 + (i * 97) % 7000 for i in range(1024)], 256, 0),
+    ([1 + (i * 97) % 7000 for i in range(1025)], 200, 0),
+    ([4000] * 16, 257, 0),
     # batch / part limits; p * W passes 2^32 (the block total itself stays an int32)
     ([(i * 2654435761) % 2**25 for i in range(4096)], 1024, 0),
     ([3000], 1024, 0),
