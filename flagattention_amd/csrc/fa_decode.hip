@@ -805,36 +805,52 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         // softmax(t) of the owned rows: row 32*wave + 16rt + i16, tokens
         // 16tt + 4G + i (8 per row and lane)
         const bool partial = vm != ~0u || t >= causal_from;  // uniform
+        // dense, full tile, both references set (uniform; the usual case):
+        // scores relative to the reference in one fma each, the running max
+        // kept absolute (the reference plus the relative max), and both row
+        // tiles in one branch-free block so that their dependency chains
+        // interleave (1% faster than one row tile after the other).  Sparse
+        // tiles are partial about half the time, where the test costs more
+        // than it saves.
+        const bool fast = kMode == kDense && !partial &&
+                          __ballot(mref[0] == ninf || mref[1] == ninf) == 0ull;
+        if (fast) {
+          float sv[2][8];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          float sv[8];
-          // dense, full tile, reference set (uniform; the usual case): scores
-          // relative to the reference in one fma each; the running max is
-          // kept absolute (the reference plus the relative max).  (Sparse
-          // tiles are partial about half the time, where the test costs more
-          // than it saves.)
-          if (kMode == kDense && !partial && __ballot(mref[rt] == ninf) == 0ull) {
+          for (int rt = 0; rt < 2; ++rt) {
             const float nmu = -mref[rt];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
               for (int i = 0; i < 4; ++i)
-                sv[4 * tt + i] = __builtin_fmaf(sacc[tt][rt][i], scale_log2, nmu);
-            const float mr = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-            mmax[rt] = fmaxf(mmax[rt], mr + mref[rt]);
+                sv[rt][4 * tt + i] = __builtin_fmaf(sacc[tt][rt][i], scale_log2, nmu);
+          }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) sv[i] = __builtin_amdgcn_exp2f(sv[i]);
-            lsum[rt] += ((sv[0] + sv[1]) + (sv[2] + sv[3])) + ((sv[4] + sv[5]) + (sv[6] + sv[7]));
+          for (int rt = 0; rt < 2; ++rt) {
+            const float mr = fmaxf(fmaxf(fmaxf(sv[rt][0], sv[rt][1]), fmaxf(sv[rt][2], sv[rt][3])),
+                                   fmaxf(fmaxf(sv[rt][4], sv[rt][5]), fmaxf(sv[rt][6], sv[rt][7])));
+            mmax[rt] = fmaxf(mmax[rt], mr + mref[rt]);
+          }
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sv[rt][i] = __builtin_amdgcn_exp2f(sv[rt][i]);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            lsum[rt] += ((sv[rt][0] + sv[rt][1]) + (sv[rt][2] + sv[rt][3])) +
+                        ((sv[rt][4] + sv[rt][5]) + (sv[rt][6] + sv[rt][7]));
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
               uintx2 w;
-              w[0] = pack_bf16x2(sv[4 * tt + 0], sv[4 * tt + 1]);
-              w[1] = pack_bf16x2(sv[4 * tt + 2], sv[4 * tt + 3]);
+              w[0] = pack_bf16x2(sv[rt][4 * tt + 0], sv[rt][4 * tt + 1]);
+              w[1] = pack_bf16x2(sv[rt][4 * tt + 2], sv[rt][4 * tt + 3]);
               *reinterpret_cast<uintx2*>(sm.p + lo.pw[tt] + rt * 1024) = w;
             }
-            continue;
           }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2 && !fast; ++rt) {
+          float sv[8];
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
