@@ -771,18 +771,16 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             constexpr int kq = decltype(kt)::value;
             if constexpr (kq + kPre < kQkSteps) {
               ka[(kq + kPre) % kRing][0] = k_read(lo, b_cur, kq + kPre, 0);
-              if constexpr (kMode != kDense)
-                ka[(kq + kPre) % kRing][1] = k_read(lo, b_cur, kq + kPre, 1);
             }
             const bf16x8 q0 = q_op(2 * kq), q1 = q_op(2 * kq + 1);
             if constexpr (!kCopiesInPv && (kq & 1) == 0 && (kq >> 1) < kCopies)
               copy_block(creq, IntTag<(kq >> 1)>{});
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 a0 = ka[kq % kRing][0], a1 = ka[kq % kRing][1];
-            // dense: the second K read of the next k-step goes between the
-            // two MFMA pairs, which spreads the LDS requests (0.5% faster)
+            // the second K read of a later k-step goes between the two MFMA
+            // pairs, which spreads the LDS requests (0.3-0.5% faster)
             auto mid_read = [&]() {
-              if constexpr (kMode == kDense && kq + kPre < kQkSteps) {
+              if constexpr (kq + kPre < kQkSteps) {
                 __builtin_amdgcn_sched_barrier(0);
                 ka[(kq + kPre) % kRing][1] = k_read(lo, b_cur, kq + kPre, 1);
                 __builtin_amdgcn_sched_barrier(0);
