@@ -1,19 +1,23 @@
 """MLA decode benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload dense|skew|sparse|sparse_fp8]
+    python bench.py --traffic-calibrate [--workload ...]   # driver for rocprofv3 --pmc passes
 
 A step is one decode of the whole batch through the public path: scheduler metadata
 (get_mla_metadata) + decode + split combine, with every input already resident in HBM.
 The default workload is BASELINE config 2 (dense bf16, B=64, h_q=128, s_q=1, lengths
 U[4096, 8192], 64-token pages through a permuted block table).  KV pools are rotated
-between steps so consecutive steps do not hit the 256 MB last-level cache.  The default
-500 warm-up steps (about 0.1 s of GPU work) bring the GPU to its steady clocks: after only
-10, the decode kernel still runs about 20% slower.
+between steps so consecutive steps do not hit the 256 MB last-level cache.  After the W
+warm-up steps a settle phase runs further untimed steps until at least SETTLE_S seconds of
+steps have run since the start of the warm-up (reported as ``settle_s``): with only a few
+warm-up steps the GPU has not reached its steady clocks and the decode kernel runs ~20%
+slower.
 
 Prints one JSON line: value = wall-clock us/step (lower is better); `roofline` is the
-decode kernel alone (HIP events around its launch on the launch stream, on every
-EVENT_EVERY-th timed step: an event pair costs each step it brackets a few us of
-dispatch gap, which would otherwise be charged to `value`), algorithmic bytes / FLOPs
+decode kernel alone (HIP events around its launch on the launch stream, on every k-th
+timed step, k = min(EVENT_EVERY, steps // MIN_EVENT_LAUNCHES) so that at least
+MIN_EVENT_LAUNCHES launches are bracketed: an event pair costs each step it brackets a few
+us of dispatch gap, which is charged to `value`), algorithmic bytes / FLOPs
 per launch over its mean duration; `cpu_baseline` is the CPU oracle
 (the reference's PyTorch math restated) timed on a bounded sample of the same workload.
 """
@@ -36,7 +40,10 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 SCALE = 192 ** -0.5
 PAGE = 64
-EVENT_EVERY = 8  # timed steps per decode launch bracketed by an event pair
+EVENT_EVERY = 8  # at most this many timed steps per decode launch bracketed by events
+MIN_EVENT_LAUNCHES = 10  # ...and at least this many bracketed launches
+SETTLE_S = 0.25  # seconds of untimed steps (warm-up included) before the timed region
+COPY_BYTES = 512 << 20  # calibration copy of --traffic-calibrate
 
 
 def workload_spec(name: str) -> dict:
@@ -214,6 +221,10 @@ def main() -> None:
                     choices=["dense", "skew", "sparse", "sparse_fp8"])
     ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-calibrate", action="store_true",
+                    help="profiling driver: a 512 MiB device copy, then --launches decode "
+                         "steps (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
+    ap.add_argument("--launches", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -221,7 +232,7 @@ def main() -> None:
               file=sys.stderr)
         raise SystemExit(2)
 
-    import flagattention_amd as fa
+    import flag_attn.mla as fa
 
     dev = torch.device("cuda:0")
     spec = workload_spec(args.workload)
@@ -236,11 +247,34 @@ def main() -> None:
         return ws.run(q, pools[c], tables[c], lens, md, ns, SCALE, spec["causal"],
                       spec["fp8"], indices, decode_events=events)
 
+    if args.traffic_calibrate:
+        # the copy's counter value over its known byte count scales the decode's values
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(args.launches):
+            step(i)
+        torch.cuda.synchronize()
+        print(f"copy_bytes={COPY_BYTES} workload={spec['name']} launches={args.launches}",
+              flush=True)
+        return
+
+    t_warm = time.perf_counter()
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    settle_steps = 0
+    while time.perf_counter() - t_warm < SETTLE_S:
+        for _ in range(20):
+            step(settle_steps)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_warm
+    every = max(1, min(EVENT_EVERY, args.steps // MIN_EVENT_LAUNCHES))
     evs = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for i in range(0, args.steps, EVENT_EVERY)}
+           for i in range(0, args.steps, every)}
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i, evs.get(i))
@@ -286,6 +320,8 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": round(settle_s, 3),
+        "settle_steps": settle_steps,
         "ms_per_step": round(us_step / 1e3, 5),
         "higher_is_better": False,
         "scaling": "weak",

@@ -1,0 +1,19 @@
+"""MLA decode operators of the ``flag_attn`` namespace.
+
+``get_mla_metadata(cache_seqlens, num_q_tokens_per_head_k, num_heads_k, num_heads_q=None,
+is_fp8_kvcache=False, topk=None)`` returns ``(tile_scheduler_metadata, num_splits)``;
+``flash_mla_with_kvcache(q, k_cache, block_table, cache_seqlens, head_dim_v,
+tile_scheduler_metadata, num_splits, softmax_scale=None, causal=False,
+is_fp8_kvcache=False, indices=None)`` returns ``(out, lse)``.  Both are implemented in
+``flagattention_amd.mla`` (validation, allocation, launch through the C ABI).
+"""
+from flagattention_amd.mla import (  # noqa: F401
+    DecodeWorkspace,
+    MLAArgumentError,
+    flash_mla_with_kvcache,
+    get_mla_metadata,
+    sparse_rows,
+)
+
+__all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "sparse_rows", "DecodeWorkspace",
+           "MLAArgumentError"]

@@ -123,7 +123,14 @@ def get_mla_metadata(
     Returns ``(tile_scheduler_metadata int32[num_parts, 8], num_splits int32[B + 1])``.
     ``num_splits`` is the exclusive prefix sum of each sequence's segment count.
     For sparse decode pass ``topk`` (every sequence then has ``ceil(topk / 64)``
-    blocks of index slots).  ``num_sm_parts`` overrides the CU-derived part count.
+    blocks of index slots) together with ``num_heads_q``: sparse work-groups hold the
+    heads of one query token, so the part count depends on the head count.
+    ``num_sm_parts`` overrides the CU-derived part count.
+
+    The returned tensors remember the batch and mode they were built for;
+    ``flash_mla_with_kvcache`` rejects them in a call of another batch or mode (dense
+    metadata drives a sparse decode into skipped segments, sparse metadata a dense one
+    into attending only the first ``ceil(topk / 64)`` pages).
     """
     _require(isinstance(cache_seqlens, torch.Tensor), "cache_seqlens must be a tensor")
     _require(cache_seqlens.dtype == torch.int32, "cache_seqlens must be int32")
@@ -135,6 +142,8 @@ def get_mla_metadata(
     if num_heads_q is not None:
         _require(num_heads_q >= 1, "num_heads_q must be >= 1")
     _require(topk is None or topk >= 1, "topk must be >= 1")
+    _require(topk is None or num_heads_q is not None,
+             "sparse metadata (topk) needs num_heads_q: parts are sized per query token")
     _require(cache_seqlens.is_cuda, "cache_seqlens must be a CUDA (HIP) tensor")
     _require(cache_seqlens.is_contiguous(), "cache_seqlens must be contiguous")
     device = cache_seqlens.device
@@ -150,7 +159,20 @@ def get_mla_metadata(
             _ptr(cache_seqlens), batch, int(topk or 0), num_sm_parts,
             overhead_blocks(topk is not None),
             _ptr(tile_md), _ptr(num_splits), _stream(device)))
+    sig = (batch, int(topk or 0))
+    tile_md._fa_mla_sig = sig
+    num_splits._fa_mla_sig = sig
     return tile_md, num_splits
+
+
+def _check_metadata_signature(tile_md, num_splits, batch, topk):
+    """Metadata from get_mla_metadata carries (batch, topk); a decode of another batch or
+    mode must not run on it.  Tensors built elsewhere carry no tag and are not checked."""
+    want = (batch, int(topk or 0))
+    for t in (tile_md, num_splits):
+        sig = getattr(t, "_fa_mla_sig", None)
+        _require(sig is None or sig == want,
+                 f"scheduler metadata was built for (batch, topk) = {sig}, this call is {want}")
 
 
 def _check_decode_args(q, k_cache, block_table, cache_seqlens, head_dim_v, tile_md,
@@ -200,6 +222,8 @@ def _check_decode_args(q, k_cache, block_table, cache_seqlens, head_dim_v, tile_
         _require(indices.shape[2] >= 1 and indices.stride(2) == 1,
                  "indices last dim must be contiguous and non-empty")
         _require(not causal, "causal masking does not apply to sparse (indices) decode")
+    _check_metadata_signature(tile_md, num_splits, batch,
+                              None if indices is None else indices.shape[2])
     tensors = [q, k_cache, block_table, cache_seqlens, tile_md, num_splits]
     if indices is not None:
         tensors.append(indices)

@@ -161,21 +161,54 @@ def attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: f
     return out, lse
 
 
+def attention_lse_lowp(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float,
+                       causal: bool, dtype: torch.dtype = torch.bfloat16
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The same attention with the reference's ``upcast=False`` arithmetic
+    (``testing/flash.py:47-75``): ``S = q k^T * sm_scale`` in ``dtype``, softmax in fp32,
+    ``P`` cast back to ``dtype``, ``P v`` in ``dtype``.  This is the ``torch_lowp`` leg of
+    the reference's accuracy rule ``max|hyp - ref| <= 2 max|lowp - ref| + 1e-5``
+    (``tests/flag_attn/test_flash_attention.py:119-127``).  Returns ``out`` (fp32 view of
+    the ``dtype`` result) and ``lse`` of the low-precision ``S``."""
+    q = q.to(dtype)
+    k = k.to(dtype)
+    v = v.to(dtype)
+    h, m, _ = q.shape
+    n = k.shape[0]
+    if n == 0:
+        return (torch.zeros((h, m, v.shape[1]), dtype=torch.float32),
+                torch.full((h, m), float("-inf")))
+    s = torch.matmul(q, k.t().contiguous()) * sm_scale
+    if causal:
+        ms = torch.arange(m).unsqueeze(-1)
+        ns = torch.arange(n)
+        s = torch.where(ms + (n - m) >= ns, s, torch.tensor(float("-inf"), dtype=dtype))
+    s = s.float()
+    lse = torch.logsumexp(s, dim=-1)
+    empty = torch.isneginf(lse)
+    p = torch.softmax(s, dim=-1, dtype=torch.float32)
+    p = torch.where(empty.unsqueeze(-1), torch.zeros_like(p), p)
+    out = torch.matmul(p.to(dtype), v).float()
+    return out, lse
+
+
 def dense_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
                      cache_seqlens: torch.Tensor, sm_scale: float, causal: bool = False,
-                     batches: Optional[Sequence[int]] = None
+                     batches: Optional[Sequence[int]] = None, lowp: bool = False
                      ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Dense paged MLA decode in fp32.  ``q [B, s_q, h_q, 576]``, bf16/fp32 cache
     ``[num_blocks, 64, 1, 576]``; returns ``out [B', s_q, h_q, 512]`` and
-    ``lse [B', h_q, s_q]`` for the sequences in ``batches`` (default: all)."""
+    ``lse [B', h_q, s_q]`` for the sequences in ``batches`` (default: all).
+    ``lowp=True``: the bf16 arithmetic of ``attention_lse_lowp`` instead."""
     bsz, s_q, h_q, _ = q.shape
     bl = list(range(bsz)) if batches is None else list(batches)
     out = torch.zeros((len(bl), s_q, h_q, D_V), dtype=torch.float32)
     lse = torch.full((len(bl), h_q, s_q), float("-inf"), dtype=torch.float32)
+    att = attention_lse_lowp if lowp else attention_lse
     for i, b in enumerate(bl):
         n = int(cache_seqlens[b])
         kv = gather_rows(k_cache, block_table, b, torch.arange(n)).float()
-        o, l = attention_lse(q[b].float().permute(1, 0, 2), kv, kv[:, :D_V], sm_scale, causal)
+        o, l = att(q[b].float().permute(1, 0, 2), kv, kv[:, :D_V], sm_scale, causal)
         out[i] = o.permute(1, 0, 2)
         lse[i] = l
     return out, lse
@@ -183,11 +216,12 @@ def dense_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.
 
 def sparse_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
                       cache_seqlens: torch.Tensor, indices: torch.Tensor, sm_scale: float,
-                      is_fp8: bool = False, batches: Optional[Sequence[int]] = None
-                      ) -> Tuple[torch.Tensor, torch.Tensor]:
+                      is_fp8: bool = False, batches: Optional[Sequence[int]] = None,
+                      lowp: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """Sparse top-k MLA decode in fp32: query token ``(b, s)`` attends to the valid
     entries of ``indices[b, s]`` (``0 <= i < cache_seqlens[b]``), each a cache row found
-    through ``block_table``; fp8 rows are decoded with ``fp8_rows_dequant``."""
+    through ``block_table``; fp8 rows are decoded with ``fp8_rows_dequant``.
+    ``lowp=True``: the bf16 arithmetic of ``attention_lse_lowp`` instead."""
     bsz, s_q, h_q, _ = q.shape
     bl = list(range(bsz)) if batches is None else list(batches)
     nblk = k_cache.shape[0]
@@ -200,7 +234,8 @@ def sparse_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch
             r = rows[i, s]
             r = r[r >= 0].long()
             kv = fp8_rows_dequant(flat[r]) if is_fp8 else flat[r].float()
-            o, l = attention_lse(q[b, s].float().unsqueeze(1), kv, kv[:, :D_V], sm_scale, False)
+            att = attention_lse_lowp if lowp else attention_lse
+            o, l = att(q[b, s].float().unsqueeze(1), kv, kv[:, :D_V], sm_scale, False)
             out[i, s] = o[:, 0]
             lse[i, :, s] = l[:, 0]
     return out, lse

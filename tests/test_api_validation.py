@@ -73,6 +73,8 @@ def test_fp8_cache_row_size():
     (dict(cache_seqlens=torch.zeros(3, dtype=torch.int32), num_q_tokens_per_head_k=128,
           num_heads_k=1, topk=0), "topk"),
     (dict(cache_seqlens=torch.zeros(3, dtype=torch.int32), num_q_tokens_per_head_k=128,
+          num_heads_k=1, topk=2048), "num_heads_q"),
+    (dict(cache_seqlens=torch.zeros(3, dtype=torch.int32), num_q_tokens_per_head_k=128,
           num_heads_k=1), "CUDA"),
 ])
 def test_metadata_rejects(kw, msg):
@@ -88,3 +90,39 @@ def test_parts_derivation():
     assert default_num_parts(256, 128, 1) == 256
     assert default_num_parts(256, 256, 1) == 128
     assert default_num_parts(4, 1024, 1) == 1
+
+
+@pytest.mark.parametrize("sig,indices", [
+    ((2, 2048), None),                                   # sparse metadata, dense call
+    ((2, 0), torch.zeros((2, 1, 8), dtype=torch.int32)),  # dense metadata, sparse call
+    ((3, 0), None),                                      # metadata of another batch
+])
+def test_decode_rejects_metadata_of_another_call(sig, indices):
+    """get_mla_metadata tags its tensors with (batch, topk); the decode checks the tag
+    before anything else touches the device."""
+    args = _dense()
+    args["tile_scheduler_metadata"]._fa_mla_sig = sig
+    args["num_splits"]._fa_mla_sig = sig
+    args["indices"] = indices
+    with pytest.raises(MLAArgumentError, match="scheduler metadata was built for"):
+        _call(**args)
+
+
+def test_flag_attn_namespace_exports_the_mla_operators():
+    """The drop-in surface: ``import flag_attn`` gives the MLA operators with the
+    FlashMLA-style signatures (src/flag_attn/__init__.py:23-29 is the export style)."""
+    import inspect
+
+    import flag_attn
+    import flag_attn.mla
+
+    assert flag_attn.get_mla_metadata is fa.get_mla_metadata
+    assert flag_attn.flash_mla_with_kvcache is fa.flash_mla_with_kvcache
+    md = inspect.signature(flag_attn.get_mla_metadata).parameters
+    assert list(md)[:6] == ["cache_seqlens", "num_q_tokens_per_head_k", "num_heads_k",
+                            "num_heads_q", "is_fp8_kvcache", "topk"]
+    dec = inspect.signature(flag_attn.flash_mla_with_kvcache).parameters
+    assert list(dec) == ["q", "k_cache", "block_table", "cache_seqlens", "head_dim_v",
+                         "tile_scheduler_metadata", "num_splits", "softmax_scale", "causal",
+                         "is_fp8_kvcache", "indices"]
+    assert dec["indices"].default is None and dec["causal"].default is False
