@@ -70,6 +70,9 @@ SIGNATURES = {
     "fa_mla_decode_sparse": (
         ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_int32, ctypes.c_void_p]),
     "fa_mla_combine": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]),
+    "fa_mla_noalloc_scratch_bytes": (ctypes.c_int64, [ctypes.POINTER(DecodeArgs), ctypes.c_int32]),
+    "fa_mla_decode_noalloc": (
+        ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_int32, ctypes.c_void_p]),
 }
 
 _lock = threading.Lock()

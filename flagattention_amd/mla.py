@@ -232,6 +232,34 @@ def _check_decode_args(q, k_cache, block_table, cache_seqlens, head_dim_v, tile_
     return batch, s_q, h_q
 
 
+def _decode_args(q, k_cache, block_table, cache_seqlens, tile_md, num_splits, out, lse,
+                 softmax_scale, causal, o_accum=None, lse_accum=None) -> "_lib.DecodeArgs":
+    """The C-ABI argument block of one decode call (indices are added by _set_indices)."""
+    batch, s_q, h_q, _ = q.shape
+    esz = k_cache.element_size()
+    return _lib.DecodeArgs(
+        q=q.data_ptr(), q_stride_b=q.stride(0), q_stride_s=q.stride(1),
+        q_stride_h=q.stride(2), kv=k_cache.data_ptr(),
+        kv_block_stride=k_cache.stride(0) * esz, kv_row_stride=k_cache.stride(1) * esz,
+        num_kv_blocks=k_cache.shape[0], block_table=block_table.data_ptr(),
+        bt_stride_b=block_table.stride(0), max_blocks_per_seq=block_table.shape[1],
+        cache_seqlens=cache_seqlens.data_ptr(), indices=None, idx_stride_b=0,
+        idx_stride_s=0, topk=0, sparse_rows=None,
+        tile_md=tile_md.data_ptr(), num_splits=num_splits.data_ptr(),
+        num_parts=tile_md.shape[0], out=out.data_ptr(), lse=lse.data_ptr(),
+        o_accum=None if o_accum is None else o_accum.data_ptr(),
+        lse_accum=None if lse_accum is None else lse_accum.data_ptr(),
+        batch=batch, s_q=s_q, h_q=h_q, softmax_scale=float(softmax_scale),
+        causal=int(bool(causal)))
+
+
+def _set_indices(args, indices) -> None:
+    args.indices = indices.data_ptr()
+    args.idx_stride_b = indices.stride(0)
+    args.idx_stride_s = indices.stride(1)
+    args.topk = indices.shape[2]
+
+
 class DecodeWorkspace:
     """Outputs and split workspace for decode steps of one shape, allocated once.
 
@@ -282,28 +310,14 @@ class DecodeWorkspace:
             softmax_scale = 1.0 / math.sqrt(D_QK)
         _require(math.isfinite(softmax_scale), "softmax_scale must be finite")
         device = q.device
-        esz = k_cache.element_size()
-        args = _lib.DecodeArgs(
-            q=q.data_ptr(), q_stride_b=q.stride(0), q_stride_s=q.stride(1),
-            q_stride_h=q.stride(2), kv=k_cache.data_ptr(),
-            kv_block_stride=k_cache.stride(0) * esz, kv_row_stride=k_cache.stride(1) * esz,
-            num_kv_blocks=k_cache.shape[0], block_table=block_table.data_ptr(),
-            bt_stride_b=block_table.stride(0), max_blocks_per_seq=block_table.shape[1],
-            cache_seqlens=cache_seqlens.data_ptr(), indices=None, idx_stride_b=0,
-            idx_stride_s=0, topk=0, sparse_rows=None,
-            tile_md=tile_scheduler_metadata.data_ptr(), num_splits=num_splits.data_ptr(),
-            num_parts=tile_scheduler_metadata.shape[0], out=self.out.data_ptr(),
-            lse=self.lse.data_ptr(), o_accum=self.o_accum.data_ptr(),
-            lse_accum=self.lse_accum.data_ptr(), batch=batch, s_q=s_q, h_q=h_q,
-            softmax_scale=float(softmax_scale), causal=int(bool(causal)))
+        args = _decode_args(q, k_cache, block_table, cache_seqlens, tile_scheduler_metadata,
+                            num_splits, self.out, self.lse, softmax_scale, causal,
+                            self.o_accum, self.lse_accum)
         lib = _lib.load()
         with torch.cuda.device(device):
             stream = _stream(device)
             if indices is not None:
-                args.indices = indices.data_ptr()
-                args.idx_stride_b = indices.stride(0)
-                args.idx_stride_s = indices.stride(1)
-                args.topk = indices.shape[2]
+                _set_indices(args, indices)
                 args.sparse_rows = self.rows.data_ptr()
                 _lib.check(lib.fa_mla_sparse_rows(ctypes.byref(args), stream))
             if decode_events is not None:
@@ -391,3 +405,47 @@ def sparse_rows(
     with torch.cuda.device(device):
         _lib.check(lib.fa_mla_sparse_rows(ctypes.byref(args), _stream(device)))
     return rows
+
+
+def decode_noalloc(
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    tile_scheduler_metadata: torch.Tensor,
+    num_splits: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    causal: bool = False,
+    is_fp8_kvcache: bool = False,
+    indices: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``flash_mla_with_kvcache`` into caller-owned ``out`` / ``lse`` through the C ABI's
+    allocation-free entry point (``fa_mla_decode_noalloc``): the split partials and gather
+    rows live in the library's own device array, so the step allocates no device memory.
+    For callers that cannot allocate (graph capture, serving loops).  Calls that overlap on
+    one device share that array and race; a shape whose workspace exceeds
+    ``FA_MLA_NOALLOC_SCRATCH_BYTES`` (64 MiB) raises ``RuntimeError``."""
+    batch, s_q, h_q = _check_decode_args(q, k_cache, block_table, cache_seqlens, D_V,
+                                         tile_scheduler_metadata, num_splits, causal,
+                                         is_fp8_kvcache, indices)
+    _require(out.dtype == torch.bfloat16 and out.shape == (batch, s_q, h_q, D_V)
+             and out.is_contiguous() and out.device == q.device,
+             "out must be contiguous bf16 [batch, s_q, h_q, 512] on q's device")
+    _require(lse.dtype == torch.float32 and lse.shape == (batch, h_q, s_q)
+             and lse.is_contiguous() and lse.device == q.device,
+             "lse must be contiguous fp32 [batch, h_q, s_q] on q's device")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D_QK)
+    _require(math.isfinite(softmax_scale), "softmax_scale must be finite")
+    args = _decode_args(q, k_cache, block_table, cache_seqlens, tile_scheduler_metadata,
+                        num_splits, out, lse, softmax_scale, causal)
+    mode = 0
+    if indices is not None:
+        _set_indices(args, indices)
+        mode = 2 if is_fp8_kvcache else 1
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.fa_mla_decode_noalloc(ctypes.byref(args), mode, _stream(q.device)))
+    return out, lse

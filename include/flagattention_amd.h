@@ -40,6 +40,9 @@ extern "C" {
 #define FA_MLA_FP8_ROW_BYTES 656 /* 512 e4m3 + 4 fp32 scales + 64 bf16   */
 #define FA_MLA_MAX_BATCH 4096
 #define FA_MLA_MAX_PARTS 1024
+/* Workspace of fa_mla_decode_noalloc: one file-scope device array of this
+ * many bytes per device the library runs on, held until the process ends. */
+#define FA_MLA_NOALLOC_SCRATCH_BYTES (64ll << 20)
 
 /* Version of this ABI (FA_ABI_VERSION of the built library). */
 int fa_abi_version(void);
@@ -165,6 +168,29 @@ int fa_mla_decode_sparse(const fa_mla_decode_args* args, int32_t fp8, void* stre
  * src/flag_attn/paged.py:366-449).
  */
 int fa_mla_combine(const fa_mla_decode_args* args, void* stream);
+
+/*
+ * Workspace bytes one fa_mla_decode_noalloc call with these arguments needs
+ * (mode as below), or -1 if the shape fields are invalid.  A call fits when
+ * this is <= FA_MLA_NOALLOC_SCRATCH_BYTES.
+ */
+int64_t fa_mla_noalloc_scratch_bytes(const fa_mla_decode_args* args, int32_t mode);
+
+/*
+ * A whole decode step that allocates nothing: for sparse modes the row
+ * translation, then the decode, then the combine -- the same kernels as
+ * fa_mla_sparse_rows + fa_mla_decode_dense / fa_mla_decode_sparse +
+ * fa_mla_combine, with the split partials and gather rows kept in the
+ * library's own device array (FA_MLA_NOALLOC_SCRATCH_BYTES per device)
+ * instead of caller workspace.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The caller passes
+ * inputs and outputs as for the other calls; o_accum, lse_accum and
+ * sparse_rows must be NULL.  mode: 0 dense, 1 sparse bf16, 2 sparse fp8.
+ * Sizes beyond the array fail with FA_ERR_INVALID_ARG.  Calls that overlap
+ * on one device (several streams or threads) share the array and race.
+ */
+int fa_mla_decode_noalloc(const fa_mla_decode_args* args, int32_t mode, void* stream);
 
 #ifdef __cplusplus
 }
