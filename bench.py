@@ -212,13 +212,149 @@ def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
                       f"scaled x{b / sample:.2f} to the full step"}
 
 
+# Grouped-query decode workloads (flag_attn.paged_attention / flash_attention decode), the
+# shapes of the reference's benchmark/paged_benchmark.py (64 query heads, group 8, head dim
+# 128, 16-token blocks, fp16; the largest batch, context 8192) and
+# benchmark/flash_decoding_benchmark.py (batch 2, 2048 / D heads, one query, long context).
+GQA_WORKLOADS = {
+    "gqa_paged": dict(name="gqa_paged_b64_h64_g8_d128_ctx8192", kind="paged", batch=64, h_q=64,
+                      group=8, d=128, block=16, ctx=8192, seed=11),
+    "gqa_splitkv": dict(name="gqa_splitkv_b2_h16_d128_ctx262144", kind="splitkv", batch=2,
+                        h_q=16, group=1, d=128, ctx=262144, seed=12),
+}
+GQA_METRIC = "GQA decode µs/step + achieved HBM GB/s (% of roofline)"
+
+
+def run_gqa(args) -> None:
+    """Grouped-query decode bench: inputs resident in HBM, the KV pool sized to the keys
+    the step reads (a permuted block table for the paged cache) and rotated between two
+    copies; the roofline kernel is the decode kernel alone (events around its launch)."""
+    import flag_attn
+    from flagattention_amd import gqa
+
+    spec = GQA_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(spec["seed"])
+    dgen = torch.Generator(device=dev).manual_seed(spec["seed"])
+    b, h_q, d, ctx = spec["batch"], spec["h_q"], spec["d"], spec["ctx"]
+    h_kv = h_q // spec["group"]
+    dt = torch.float16
+    scale = d ** -0.5
+    copies = []
+    for _ in range(2):
+        if spec["kind"] == "paged":
+            bs = spec["block"]
+            nblk = -(-ctx // bs)
+            pool = b * nblk
+            q = torch.empty((b, h_q, d), dtype=dt, device=dev).uniform_(-scale, scale,
+                                                                        generator=dgen)
+            kc = torch.empty((pool, h_kv, bs, d), dtype=dt, device=dev).uniform_(
+                -scale, scale, generator=dgen)
+            vc = torch.empty_like(kc).uniform_(-scale, scale, generator=dgen)
+            bt = torch.randperm(pool, generator=gen).to(torch.int32).view(b, nblk).to(dev)
+            lens = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+            copies.append((q, kc, vc, lens, bt))
+        else:
+            q = torch.randn((b, h_q, 1, d), generator=dgen, device=dev).to(dt)
+            k = torch.randn((b, h_kv, ctx, d), generator=dgen, device=dev).to(dt)
+            v = torch.randn((b, h_kv, ctx, d), generator=dgen, device=dev).to(dt)
+            copies.append((q, k, v))
+
+    def step(i, events=None):
+        gqa.timing_events = events
+        c = copies[i % 2]
+        if spec["kind"] == "paged":
+            q, kc, vc, lens, bt = c
+            return flag_attn.paged_attention(q, kc, vc, lens, bt, scale, ctx)
+        q, k, v = c
+        return flag_attn.flash_attention(q, k, v, False)
+
+    t_warm = time.perf_counter()
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    settle_steps = 0
+    while time.perf_counter() - t_warm < SETTLE_S:
+        for _ in range(20):
+            step(settle_steps)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_warm
+    every = max(1, min(EVENT_EVERY, args.steps // MIN_EVENT_LAUNCHES))
+    evs = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for i in range(0, args.steps, every)}
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, evs.get(i))
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) / args.steps * 1e6
+    dec = sorted(s.elapsed_time(e) for s, e in evs.values())
+    dec_us = sum(dec) / len(dec) * 1e3
+    kv_bytes = b * ctx * h_kv * d * 2 * 2
+    nbytes = kv_bytes + 2 * b * h_q * d * 2 + (b * (-(-ctx // spec.get("block", ctx))) * 4
+                                                  if spec["kind"] == "paged" else 0)
+    flops = 2.0 * b * h_q * 2 * ctx * d  # QK and PV, as benchmark/paged_benchmark.py:198
+    gbs = nbytes / (dec_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = gqa_cpu_baseline(spec, copies[0], scale)
+    rec = {
+        "metric": GQA_METRIC, "value": round(us_step, 2), "unit": "µs/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "settle_s": round(settle_s, 3),
+        "settle_steps": settle_steps, "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": spec["name"], "batch": b, "h_q": h_q, "h_kv": h_kv, "d": d,
+                   "ctx": ctx, "block_size": spec.get("block")},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gqa_decode_kernel", "kernel_launches_timed": len(dec),
+                     "kernel_us_mean": round(dec_us, 2), "bytes_per_launch": nbytes,
+                     "flops_per_launch": flops,
+                     "tflops": round(flops / (dec_us * 1e-6) / 1e12, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def gqa_cpu_baseline(spec, inputs, scale) -> dict:
+    """The oracle (the reference's testing/paged.py and testing/flash.py math, restated)
+    on one sequence of the workload, scaled to the full step."""
+    from oracle import gqa_oracle as go
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    b = spec["batch"]
+    if spec["kind"] == "paged":
+        q, kc, vc, lens, bt = inputs
+        need = torch.unique(bt[:1].flatten()).long()
+        remap = torch.full((kc.shape[0],), -1, dtype=torch.long, device=kc.device)
+        remap[need] = torch.arange(need.numel(), device=kc.device)
+        args = (q[:1].cpu(), kc[need].cpu(), vc[need].cpu(),
+                remap[bt[:1].long()].to(torch.int32).cpu(), lens[:1].cpu(), scale)
+        fn = lambda: go.paged_attention_ref(*args)  # noqa: E731
+    else:
+        q, k, v = inputs
+        args = (q[:1].cpu(), k[:1].cpu(), v[:1].cpu())
+        fn = lambda: go.flash_attention_ref(*args, False, upcast=True)  # noqa: E731
+    fn()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": round(t * b * 1e6, 1), "unit": "µs/step", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"1 of {b} sequences of {spec['name']}, median of 3, "
+                                      f"scaled x{b} to the full step"}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--workload", default="dense",
-                    choices=["dense", "skew", "sparse", "sparse_fp8"])
+                    choices=["dense", "skew", "sparse", "sparse_fp8"] + list(GQA_WORKLOADS))
     ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-calibrate", action="store_true",
@@ -231,6 +367,10 @@ def main() -> None:
               "(batch sharding across GPUs needs no exchange: run one process per GPU).",
               file=sys.stderr)
         raise SystemExit(2)
+
+    if args.workload in GQA_WORKLOADS:
+        run_gqa(args)
+        return
 
     import flag_attn.mla as fa
 

@@ -1,10 +1,13 @@
-"""flagattention_amd: MLA decode for AMD MI355X (gfx950).
+"""flagattention_amd: attention decode for AMD MI355X (gfx950).
 
-Dense and sparse top-k decode over a paged latent KV cache (576-dim QK, 512-dim V, one
-shared latent KV head), split-KV scheduling and an LSE-weighted combine, as hand-written
-HIP kernels behind a C ABI (include/flagattention_amd.h).  This module is the Python
-operator surface; there is no CPU fallback.
+MLA decode -- dense and sparse top-k over a paged latent KV cache (576-dim QK, 512-dim V,
+one shared latent KV head), split-KV scheduling and an LSE-weighted combine -- and
+grouped-query decode over paged or contiguous caches, as hand-written HIP kernels behind
+a C ABI (include/flagattention_amd.h).  This module is the Python operator surface; there
+is no CPU fallback.
 """
+from .errors import ArgumentError  # noqa: F401
+from .gqa import flash_attention, flash_attention_split_kv, paged_attention  # noqa: F401
 from .mla import (  # noqa: F401
     DecodeWorkspace,
     MLAArgumentError,
@@ -14,5 +17,6 @@ from .mla import (  # noqa: F401
 )
 
 __all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "sparse_rows", "DecodeWorkspace",
-           "MLAArgumentError"]
+           "MLAArgumentError", "ArgumentError", "paged_attention", "flash_attention_split_kv",
+           "flash_attention"]
 __version__ = "0.1.0"

@@ -9,7 +9,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflagattention_amd.so")
 
 FA_OK = 0
@@ -54,6 +54,49 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class GqaArgs(ctypes.Structure):
+    """Mirror of ``fa_gqa_decode_args`` (field order and types must match the header)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("q_stride_b", ctypes.c_int64),
+        ("q_stride_h", ctypes.c_int64),
+        ("q_stride_m", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_stride_0", ctypes.c_int64),
+        ("k_stride_h", ctypes.c_int64),
+        ("k_stride_t", ctypes.c_int64),
+        ("v_stride_0", ctypes.c_int64),
+        ("v_stride_h", ctypes.c_int64),
+        ("v_stride_t", ctypes.c_int64),
+        ("block_table", ctypes.c_void_p),
+        ("bt_stride_b", ctypes.c_int64),
+        ("max_blocks_per_seq", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int64),
+        ("seqlens", ctypes.c_void_p),
+        ("n", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+        ("o_stride_b", ctypes.c_int64),
+        ("o_stride_h", ctypes.c_int64),
+        ("o_stride_m", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
+        ("o_part", ctypes.c_void_p),
+        ("lse_part", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("h_q", ctypes.c_int32),
+        ("h_kv", ctypes.c_int32),
+        ("m", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("split_tokens", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 # name -> (restype, argtypes) for every symbol declared in the header
 SIGNATURES = {
     "fa_abi_version": (ctypes.c_int, []),
@@ -70,6 +113,9 @@ SIGNATURES = {
     "fa_mla_decode_sparse": (
         ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_int32, ctypes.c_void_p]),
     "fa_mla_combine": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]),
+    "fa_gqa_decode_args_size": (ctypes.c_int64, []),
+    "fa_gqa_decode": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),
+    "fa_gqa_combine": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),
     "fa_mla_noalloc_scratch_bytes": (ctypes.c_int64, [ctypes.POINTER(DecodeArgs), ctypes.c_int32]),
     "fa_mla_decode_noalloc": (
         ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_int32, ctypes.c_void_p]),
@@ -104,6 +150,11 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(
                 f"flagattention_amd: fa_mla_decode_args is {size} bytes in the library, "
                 f"{ctypes.sizeof(DecodeArgs)} in the binding")
+        gsize = lib.fa_gqa_decode_args_size()
+        if gsize != ctypes.sizeof(GqaArgs):
+            raise RuntimeError(
+                f"flagattention_amd: fa_gqa_decode_args is {gsize} bytes in the library, "
+                f"{ctypes.sizeof(GqaArgs)} in the binding")
         _lib = lib
         return lib
 

@@ -33,3 +33,7 @@ extern "C" int fa_device_cu_count(int device, int32_t* cu_count) {
   *cu_count = v;
   return FA_OK;
 }
+
+extern "C" int64_t fa_gqa_decode_args_size(void) {
+  return static_cast<int64_t>(sizeof(fa_gqa_decode_args));
+}

@@ -1,0 +1,124 @@
+// Wave-level helpers shared by the gfx950 decode kernels: wait counters,
+// barriers, lane ids, transposing LDS reads and cross-lane reductions.
+#pragma once
+
+#include <utility>
+
+#include "fa_common.h"
+
+namespace fa {
+
+// Load through the scalar unit (constant address space): for wave-uniform
+// metadata, so the value arrives via lgkmcnt and never forces a vmcnt wait on
+// the tile copies in flight.
+template <typename T>
+__device__ inline T sload(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
+__device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
+// Work-group barrier that also fences the instruction scheduler: the phases
+// between barriers are laid out by hand, so nothing may move across.
+__device__ inline void barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  wait_lds();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt low bits [3:0], high bits [15:14]).
+template <int N>
+__device__ inline void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Wave index as a scalar (the compiler cannot tell that threadIdx.x / 64 is
+// uniform across a wave; LDS addresses derived from it must be scalars).
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+// Lane index computed afresh where it is used: volatile asm is neither
+// hoisted nor merged with an earlier copy, so the values derived from it are
+// rebuilt in place instead of being kept (and spilled) across the kernel.
+__device__ inline int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// LDS transpose read (ds_read_b64_tr_b16).  Within each 16-lane group, result
+// lane i, element e comes from source lane 4e + i/4, element i%4: four lanes
+// pointing at 4 consecutive dims of token row e give every lane one dim of 4
+// consecutive tokens (see the V^T operand addressing in the kernel).
+__device__ inline bf16x4 lds_read_tr4(const unsigned char* p) {
+  typedef short shortx4 __attribute__((ext_vector_type(4)));
+  shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS shortx4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Values that are uniform but may have been computed in vector registers are
+// moved to scalars before they form a buffer resource (a vector resource
+// would need a loop over lanes).
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ inline const unsigned char* uniform(const unsigned char* p) {
+  const unsigned long long v = reinterpret_cast<unsigned long long>(p);
+  const unsigned int lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v));
+  const unsigned int hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned int>(v >> 32));
+  return reinterpret_cast<const unsigned char*>((static_cast<unsigned long long>(hi) << 32) | lo);
+}
+
+// Max / sum with the lane 16 (32) positions away: gfx950 lane-swap VALU ops
+// (v_permlane16_swap / v_permlane32_swap on two copies of x leave the two
+// partners' values in the two outputs), no LDS traffic.  The outputs are
+// copied to scalars before reinterpretation: a bit cast taken directly on a
+// vector element reads element 0 with this compiler.
+__device__ inline floatx2 swap16(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  floatx2 o;
+  o[0] = __uint_as_float(r0);
+  o[1] = __uint_as_float(r1);
+  return o;
+}
+__device__ inline floatx2 swap32(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  floatx2 o;
+  o[0] = __uint_as_float(r0);
+  o[1] = __uint_as_float(r1);
+  return o;
+}
+__device__ inline float max_xor16(float x) {
+  const floatx2 v = swap16(x);
+  return fmaxf(v[0], v[1]);
+}
+__device__ inline float max_xor32(float x) {
+  const floatx2 v = swap32(x);
+  return fmaxf(v[0], v[1]);
+}
+__device__ inline float sum_xor16(float x) {
+  const floatx2 v = swap16(x);
+  return v[0] + v[1];
+}
+__device__ inline float sum_xor32(float x) {
+  const floatx2 v = swap32(x);
+  return v[0] + v[1];
+}
+
+template <int V>
+struct IntTag {
+  static constexpr int value = V;
+};
+
+// f(IntTag<0>{}), ..., f(IntTag<N-1>{}): an unrolled loop whose index is a
+// compile-time constant (needed for instruction immediates).
+template <typename F, int... Is>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(IntTag<Is>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+}  // namespace fa

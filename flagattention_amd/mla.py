@@ -31,6 +31,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
+from .errors import ArgumentError
 
 PAGE_SIZE = 64
 D_QK = 576
@@ -59,7 +60,7 @@ def overhead_blocks(sparse: bool) -> int:
     return 0 if sparse else FIXED_OVERHEAD_BLOCKS
 
 
-class MLAArgumentError(ValueError, AssertionError):
+class MLAArgumentError(ArgumentError):
     """Invalid argument to an MLA operator (raised before any kernel launch)."""
 
 

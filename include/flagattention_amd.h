@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 #define FA_OK 0
 #define FA_ERR_INVALID_ARG (-1) /* shape / size / pointer check failed   */
@@ -191,6 +191,73 @@ int64_t fa_mla_noalloc_scratch_bytes(const fa_mla_decode_args* args, int32_t mod
  * on one device (several streams or threads) share the array and race.
  */
 int fa_mla_decode_noalloc(const fa_mla_decode_args* args, int32_t mode, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Grouped-query decode (MHA / GQA / MQA) over a paged or contiguous cache:
+ * the HIP path behind flag_attn.paged_attention, flag_attn.flash_attention_split_kv
+ * and the decode branch of flag_attn.flash_attention.
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Element strides are in elements of the tensors' dtype (fp16 or bf16, the
+ * same for q, k, v and out); every last dimension is contiguous and rows are
+ * 16-byte aligned.
+ */
+typedef struct fa_gqa_decode_args {
+  /* q: [batch][h_q][m][d] (strides over batch, head, query position) */
+  const void* q;
+  int64_t q_stride_b, q_stride_h, q_stride_m;
+  /* k, v: paged (block_table != NULL): [num_blocks][h_kv][block_size][d],
+   *       strides over (block, head, token);
+   *       contiguous: [batch][h_kv][n][d], strides over (batch, head, token) */
+  const void* k;
+  const void* v;
+  int64_t k_stride_0, k_stride_h, k_stride_t;
+  int64_t v_stride_0, v_stride_h, v_stride_t;
+  /* paged cache only: block_table int32 [batch][max_blocks_per_seq]; token j of
+   * sequence b is row j % block_size of page block_table[b][j / block_size];
+   * a page id outside [0, num_blocks) reads as a masked key */
+  const int32_t* block_table;
+  int64_t bt_stride_b;
+  int32_t max_blocks_per_seq;
+  int32_t block_size;
+  int64_t num_blocks;
+  /* keys per sequence: seqlens int32 [batch] (required for a paged cache), or
+   * n for every sequence when seqlens is NULL */
+  const int32_t* seqlens;
+  int32_t n;
+  /* out: [batch][h_q][m][d] (strides over batch, head, query position) */
+  void* out;
+  int64_t o_stride_b, o_stride_h, o_stride_m;
+  float* lse;      /* optional fp32 [batch][h_q][m] (natural log) */
+  float* o_part;   /* split workspace fp32 [batch][h_q][m][num_splits][d] */
+  float* lse_part; /* fp32 [batch][h_q][m][num_splits] */
+  int32_t batch, h_q, h_kv, m, d;
+  /* split s covers keys [s * split_tokens, (s + 1) * split_tokens) */
+  int32_t num_splits, split_tokens;
+  float scale;
+  int32_t causal; /* bottom-right aligned: query position i sees keys <= n - m + i */
+  int32_t dtype;  /* 0 fp16, 1 bf16 */
+} fa_gqa_decode_args;
+
+/* sizeof(fa_gqa_decode_args) as compiled into the library. */
+int64_t fa_gqa_decode_args_size(void);
+
+/*
+ * Decode: with num_splits == 1 writes out (and lse if given); otherwise the
+ * per-split partials (o_part normalised per split, lse_part) for
+ * fa_gqa_combine.  Head dims 16, 32, 64, 128, 256.
+ * Replaces _paged_attn_kernel, src/flag_attn/paged.py:218-363 (paged) and
+ * _fwd_split_kv_kernel, src/flag_attn/split_kv.py:28-174 (contiguous).
+ */
+int fa_gqa_decode(const fa_gqa_decode_args* args, void* stream);
+
+/*
+ * LSE-weighted merge of the split partials into out (and lse if given).
+ * Replaces _paged_attn_v2_reduce_kernel, src/flag_attn/paged.py:366-449 and
+ * _fwd_combine_kv_splits, src/flag_attn/split_kv.py:176-241.
+ */
+int fa_gqa_combine(const fa_gqa_decode_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,191 @@
+"""GPU parity of the grouped-query decode path (flag_attn.paged_attention,
+flag_attn.flash_attention_split_kv, flag_attn.flash_attention) against the CPU oracle.
+
+The sweeps are the reference's own: ``tests/flag_attn/test_paged_attention.py:79-157``
+(fp16, uniform(+-D^-0.5) inputs, block tables drawn with replacement, ``allclose(atol=2e-3,
+rtol=1e-5)`` against ``testing.paged_attention``) and
+``tests/flag_attn/test_flash_attention.py:82-127`` (``test_attention_splitkv``: scale 10,
+BHTD / BTHD strides, fp16 / bf16, causal or not, the rule
+``max|hyp - ref| <= 2 max|torch_lowp - ref| + 1e-5``).  Inputs are seeded here (the
+reference's paged tests are not).  Caches are generated on the GPU; the oracle gets CPU
+copies of the pages the block tables name.
+"""
+import pytest
+import torch
+
+import flag_attn
+from oracle import gqa_oracle as go
+from tests._helpers import DEV, need_gpu, say
+
+pytestmark = pytest.mark.gpu
+NUM_BLOCKS = 1000
+CACHE_BYTES = 256 << 20  # per cache; fewer pages than NUM_BLOCKS when they are large
+
+
+def base_paged_attention(num_seqs, num_query_heads, query_group_size, head_size, block_size,
+                         max_seq_len, num_splits=0, dtype=torch.float16, seed=0):
+    need_gpu()
+    say(f"paged seqs={num_seqs} H={num_query_heads} g={query_group_size} D={head_size} "
+        f"bs={block_size} len={max_seq_len} splits={num_splits} {dtype}")
+    gen = torch.Generator().manual_seed(seed)
+    dgen = torch.Generator(device=DEV).manual_seed(seed)
+    num_kv_heads = num_query_heads // query_group_size
+    context_lens = torch.randint(1, max_seq_len, (num_seqs,), generator=gen, dtype=torch.int32)
+    context_lens[0] = max_seq_len
+    max_context_len = int(context_lens.max())
+    max_blocks = (max_context_len + block_size - 1) // block_size
+    page_bytes = num_kv_heads * block_size * head_size * 2
+    nblocks = max(64, min(NUM_BLOCKS, CACHE_BYTES // page_bytes))
+    scale = head_size ** -0.5
+    q = torch.empty((num_seqs, num_query_heads, head_size), device=DEV, dtype=dtype)
+    q.uniform_(-scale, scale, generator=dgen)
+    k_cache = torch.empty((nblocks, num_kv_heads, block_size, head_size), device=DEV, dtype=dtype)
+    k_cache.uniform_(-scale, scale, generator=dgen)
+    v_cache = torch.empty_like(k_cache).uniform_(-scale, scale, generator=dgen)
+    block_tables = torch.randint(0, nblocks, (num_seqs, max_blocks), generator=gen,
+                                 dtype=torch.int32)
+    out = flag_attn.paged_attention(q, k_cache, v_cache, context_lens.to(DEV),
+                                    block_tables.to(DEV), scale, max_context_len, num_splits)
+    torch.cuda.synchronize()
+    # oracle on the pages the tables name (remapped onto a compact pool)
+    need = torch.unique(block_tables.flatten()).long()
+    remap = torch.full((nblocks,), -1, dtype=torch.long)
+    remap[need] = torch.arange(need.numel())
+    kc = k_cache[need.to(DEV)].cpu()
+    vc = v_cache[need.to(DEV)].cpu()
+    bt = remap[block_tables.long()].to(torch.int32)
+    ref = go.paged_attention_ref(q.cpu(), kc, vc, bt, context_lens, scale)
+    err = float((out.cpu().float() - ref.float()).abs().max())
+    say(f"  max |out - ref| = {err:.3e}")
+    assert torch.allclose(out.cpu(), ref, atol=2e-3, rtol=1e-5)
+
+
+@pytest.mark.parametrize("num_seqs", [1, 32])
+@pytest.mark.parametrize("num_query_heads", [64])
+@pytest.mark.parametrize("query_group_size", [1, 8])
+@pytest.mark.parametrize("head_size", [64, 128])
+@pytest.mark.parametrize("block_size", [16, 128, 256])
+@pytest.mark.parametrize("max_seq_len", [512, 4096])
+def test_paged_attention_default(num_seqs, num_query_heads, query_group_size, head_size,
+                                 block_size, max_seq_len):
+    base_paged_attention(num_seqs, num_query_heads, query_group_size, head_size, block_size,
+                         max_seq_len, seed=num_seqs * 7 + head_size + block_size + max_seq_len)
+
+
+@pytest.mark.parametrize("num_seqs", [1, 16])
+@pytest.mark.parametrize("num_query_heads", [64])
+@pytest.mark.parametrize("query_group_size", [1, 8])
+@pytest.mark.parametrize("head_size", [32, 64])
+@pytest.mark.parametrize("block_size", [16])
+@pytest.mark.parametrize("max_seq_len", [2048])
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_paged_attention_by_num_splits(num_seqs, num_query_heads, query_group_size, head_size,
+                                       block_size, max_seq_len, num_splits):
+    base_paged_attention(num_seqs, num_query_heads, query_group_size, head_size, block_size,
+                         max_seq_len, num_splits, seed=num_splits * 13 + num_seqs + head_size)
+
+
+@pytest.mark.parametrize("num_seqs, num_query_heads, query_group_size, head_size, block_size, "
+                         "max_seq_len, num_splits", [
+                             (1, 12, 1, 64, 16, 2, 0),
+                             (16, 64, 8, 32, 16, 2048, 2),
+                             (16, 64, 1, 64, 16, 2048, 6),
+                         ])
+def test_paged_attention_by_case(num_seqs, num_query_heads, query_group_size, head_size,
+                                 block_size, max_seq_len, num_splits):
+    base_paged_attention(num_seqs, num_query_heads, query_group_size, head_size, block_size,
+                         max_seq_len, num_splits, seed=5)
+
+
+@pytest.mark.parametrize("head_size,group,dtype", [
+    (16, 4, torch.float16), (256, 2, torch.float16), (128, 8, torch.bfloat16),
+    (256, 1, torch.bfloat16), (32, 16, torch.bfloat16),
+])
+@pytest.mark.parametrize("num_splits", [0, 3])
+def test_paged_attention_more_shapes(head_size, group, dtype, num_splits):
+    """Head dims 16 and 256, bf16, and query groups beyond the reference's sweep (16 rows
+    per work-group at group 16)."""
+    base_paged_attention(8, 32, group, head_size, 16, 1500, num_splits, dtype=dtype,
+                         seed=head_size + group)
+
+
+def test_paged_attention_bad_page_is_masked():
+    """A block-table entry outside the cache reads as a masked key instead of faulting."""
+    need_gpu()
+    gen = torch.Generator().manual_seed(3)
+    h, d, bs = 8, 64, 16
+    kc = torch.randn((10, h, bs, d), generator=gen).half()
+    vc = torch.randn((10, h, bs, d), generator=gen).half()
+    q = torch.randn((1, h, d), generator=gen).half()
+    bt = torch.tensor([[0, 1000, 2]], dtype=torch.int32)
+    lens = torch.tensor([48], dtype=torch.int32)
+    out = flag_attn.paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), lens.to(DEV), bt.to(DEV),
+                                    d ** -0.5, 48, 1)
+    keep = torch.tensor([[0, 2]], dtype=torch.int32)  # the same keys without the bad page
+    ref_lens = torch.tensor([32], dtype=torch.int32)
+    ref = go.paged_attention_ref(q, kc, vc, keep, ref_lens, d ** -0.5)
+    assert torch.allclose(out.cpu(), ref, atol=2e-3, rtol=1e-5)
+
+
+SPLITKV_SHAPES = [
+    (2, 4, 4, 1, 612, 128), (2, 4, 4, 1, 1034, 64), (2, 4, 4, 1, 2048, 32),
+    (2, 4, 4, 1, 4096, 16), (2, 4, 4, 1, 4001, 32), (2, 4, 4, 1, 4096, 64),
+    (2, 4, 4, 2, 4000, 128), (1, 2, 2, 4, 8202, 16), (1, 2, 2, 1, 8192, 32),
+    (2, 4, 2, 1, 612, 128), (2, 4, 1, 1, 1034, 64), (2, 4, 2, 1, 2048, 32),
+    (2, 4, 1, 1, 4096, 16), (2, 4, 2, 1, 4001, 32), (2, 4, 1, 1, 4096, 64),
+    (2, 4, 2, 2, 4000, 128), (1, 2, 1, 4, 8202, 16), (1, 2, 1, 1, 8192, 32),
+]
+
+
+def _splitkv_inputs(B, Hq, Hk, M, N, D, dtype, stride_order, scale, seed):
+    gen = torch.Generator().manual_seed(seed)
+    if stride_order == "BHTD":
+        q = torch.empty((B, Hq, M, D)).normal_(0.0, scale, generator=gen)
+        k = torch.empty((B, Hk, N, D)).normal_(0.0, scale, generator=gen)
+        v = torch.empty((B, Hk, N, D)).normal_(0.0, scale, generator=gen)
+        return q.to(dtype), k.to(dtype), v.to(dtype)
+    q = torch.empty((B, M, Hq, D)).normal_(0.0, scale, generator=gen).transpose(1, 2)
+    k = torch.empty((B, N, Hk, D)).normal_(0.0, scale, generator=gen).transpose(1, 2)
+    v = torch.empty((B, N, Hk, D)).normal_(0.0, scale, generator=gen).transpose(1, 2)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def _max_diff(a, b):
+    return float((a.float() - b.float()).abs().max())
+
+
+@pytest.mark.parametrize("scale", [10.0])
+@pytest.mark.parametrize("B, Hq, Hk, M, N, D", SPLITKV_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("stride_order", ["BHTD", "BTHD"])
+def test_attention_splitkv(B, Hq, Hk, M, N, D, causal, stride_order, dtype, scale):
+    need_gpu()
+    q, k, v = _splitkv_inputs(B, Hq, Hk, M, N, D, dtype, stride_order, scale, 10086 + N + M)
+    o_ref, _ = go.flash_attention_ref(q, k, v, causal, upcast=True)
+    o_torch, _ = go.flash_attention_ref(q, k, v, causal, upcast=False)
+    # the reference test calls flash_attention, which takes its split-KV path at these shapes
+    o_hyp = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal).cpu()
+    torch_max_diff = _max_diff(o_torch, o_ref)
+    hyp_max_diff = _max_diff(o_hyp, o_ref)
+    assert o_hyp.dtype == dtype and o_hyp.shape == q.shape
+    assert hyp_max_diff <= 2 * torch_max_diff + 1e-5, (hyp_max_diff, torch_max_diff)
+
+
+@pytest.mark.parametrize("B, Hq, Hk, M, N, D", SPLITKV_SHAPES[::3])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_attention_split_kv_and_lse(B, Hq, Hk, M, N, D, causal):
+    """flash_attention_split_kv gives the same o; flash_attention's log normaliser matches
+    the oracle's logsumexp."""
+    need_gpu()
+    q, k, v = _splitkv_inputs(B, Hq, Hk, M, N, D, torch.bfloat16, "BHTD", 1.0, N)
+    o_ref, lse_ref = go.flash_attention_ref(q, k, v, causal, upcast=True)
+    o_torch, _ = go.flash_attention_ref(q, k, v, causal, upcast=False)
+    o1 = flag_attn.flash_attention_split_kv(q.to(DEV), k.to(DEV), v.to(DEV), causal).cpu()
+    o2, lse, tot, seed, off = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                                        return_log_normalizer=True)
+    assert tot is None and seed is None and off is None
+    assert torch.equal(o1, o2.cpu())
+    assert _max_diff(o1, o_ref) <= 2 * _max_diff(o_torch, o_ref) + 1e-5
+    assert lse.shape == (B, Hq, M) and lse.dtype == torch.float32
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
