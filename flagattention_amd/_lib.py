@@ -113,6 +113,11 @@ SIGNATURES = {
     "fa_mla_decode_sparse": (
         ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_int32, ctypes.c_void_p]),
     "fa_mla_combine": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]),
+    "fa_mla_kvcache_write": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+         ctypes.c_int32, ctypes.c_void_p]),
     "fa_gqa_decode_args_size": (ctypes.c_int64, []),
     "fa_gqa_decode": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),
     "fa_gqa_combine": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),

@@ -1,0 +1,97 @@
+// KV-cache write path for the MLA decode layouts: new tokens' latent (512) and
+// rope (64) vectors go to their physical rows, either as 1152-byte bf16 rows or
+// quantised into the 656-byte fp8 rows that sparse fp8 decode reads:
+//   bytes [0, 512)    e4m3 ("fn") codes of the 512 latent dims,
+//   bytes [512, 528)  one fp32 scale per 128 dims, scale = amax / 448 (1 for
+//                     an all-zero tile), code = e4m3(clamp(x / scale, +-448)),
+//   bytes [528, 656)  the 64 rope dims in bf16.
+// One wave per token: lane l holds latent dims 8l..8l+7; the 16 lanes of a
+// 128-dim tile reduce its amax with four lane exchanges.
+//
+// The reference has no cache writer (its tests fill caches in place); the
+// row formats are the ones fa_mla_decode_dense / fa_mla_decode_sparse read.
+#include "fa_common.h"
+
+namespace fa {
+namespace {
+
+__device__ inline unsigned int fp8x2(float a, float b) {
+  // two fp32 -> two OCP e4m3 codes in the low 16 bits (round to nearest even)
+  return static_cast<unsigned int>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xFFFFu;
+}
+
+__global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
+    const bf16* __restrict__ kv_c, long long kv_c_stride, const bf16* __restrict__ k_pe,
+    long long k_pe_stride, const long long* __restrict__ slot_mapping, int num_tokens,
+    unsigned char* __restrict__ cache, long long block_stride, long long row_stride,
+    long long num_rows, int fp8) {
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= num_tokens) return;
+  const int lane = threadIdx.x & 63;
+  const long long slot = slot_mapping[tok];
+  if (slot < 0 || slot >= num_rows) return;  // padding tokens / slots outside the cache
+  unsigned char* row = cache + (slot >> 6) * block_stride + (slot & 63) * row_stride;
+  const bf16x8 x = *reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane);
+  bf16x8 pe{};
+  if (lane < 8) pe = *reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane);
+  if (!fp8) {
+    *reinterpret_cast<bf16x8*>(row + 16 * lane) = x;
+    if (lane < 8) *reinterpret_cast<bf16x8*>(row + 1024 + 16 * lane) = pe;
+    return;
+  }
+  float f[8];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[i] = static_cast<float>(x[i]);
+    amax = fmaxf(amax, fabsf(f[i]));
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float scale = amax > 0.f ? amax / 448.f : 1.f;
+  uintx2 codes;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(f[4 * w + i] / scale, -448.f), 448.f);
+    codes[w] = fp8x2(v[0], v[1]) | (fp8x2(v[2], v[3]) << 16);
+  }
+  *reinterpret_cast<uintx2*>(row + 8 * lane) = codes;
+  if ((lane & 15) == 0) *reinterpret_cast<float*>(row + 512 + 4 * (lane >> 4)) = scale;
+  if (lane < 8) *reinterpret_cast<bf16x8*>(row + 528 + 16 * lane) = pe;
+}
+
+}  // namespace
+}  // namespace fa
+
+extern "C" int fa_mla_kvcache_write(const void* kv_c, int64_t kv_c_stride, const void* k_pe,
+                                    int64_t k_pe_stride, const int64_t* slot_mapping,
+                                    int32_t num_tokens, void* kv_cache, int64_t kv_block_stride,
+                                    int64_t kv_row_stride, int64_t num_kv_blocks, int32_t fp8,
+                                    void* stream) {
+  FA_CHECK_ARG(num_tokens >= 0, "num_tokens %d < 0", num_tokens);
+  if (num_tokens == 0) return FA_OK;
+  FA_CHECK_ARG(kv_c && k_pe && slot_mapping && kv_cache, "NULL pointer");
+  FA_CHECK_ARG((reinterpret_cast<uintptr_t>(kv_c) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(k_pe) & 15) == 0 && kv_c_stride % 8 == 0 &&
+                   k_pe_stride % 8 == 0,
+               "kv_c / k_pe rows must be 16-byte aligned");
+  FA_CHECK_ARG((reinterpret_cast<uintptr_t>(kv_cache) & 15) == 0 && kv_block_stride % 16 == 0 &&
+                   kv_row_stride % 16 == 0,
+               "cache rows must be 16-byte aligned");
+  FA_CHECK_ARG(num_kv_blocks >= 1, "num_kv_blocks %lld < 1", static_cast<long long>(num_kv_blocks));
+  FA_CHECK_ARG(kv_row_stride >= (fp8 ? FA_MLA_FP8_ROW_BYTES : 2 * FA_MLA_D_QK),
+               "cache row stride %lld smaller than the row", static_cast<long long>(kv_row_stride));
+  const dim3 grid(static_cast<unsigned>((num_tokens + 3) / 4));
+  hipLaunchKernelGGL(fa::mla_kvcache_write_kernel, grid, dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const fa::bf16*>(kv_c),
+                     static_cast<long long>(kv_c_stride), static_cast<const fa::bf16*>(k_pe),
+                     static_cast<long long>(k_pe_stride),
+                     reinterpret_cast<const long long*>(slot_mapping), num_tokens,
+                     static_cast<unsigned char*>(kv_cache), static_cast<long long>(kv_block_stride),
+                     static_cast<long long>(kv_row_stride),
+                     static_cast<long long>(num_kv_blocks) * fa::kPage, fp8 ? 1 : 0);
+  FA_CHECK_HIP(hipGetLastError());
+  return FA_OK;
+}

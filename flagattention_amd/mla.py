@@ -450,3 +450,59 @@ def decode_noalloc(
     with torch.cuda.device(q.device):
         _lib.check(lib.fa_mla_decode_noalloc(ctypes.byref(args), mode, _stream(q.device)))
     return out, lse
+
+
+def concat_and_cache_mla(
+    kv_c: torch.Tensor,
+    k_pe: torch.Tensor,
+    kv_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    is_fp8_kvcache: bool = False,
+) -> None:
+    """Write new tokens into the paged latent cache (in place).
+
+    kv_c          bf16 [T, 512] latent vectors, k_pe bf16 [T, 64] rope vectors
+    kv_cache      bf16 [num_blocks, 64, 1, 576], or fp8 rows uint8 [num_blocks, 64, 1, 656]
+    slot_mapping  int32 / int64 [T]: physical row page * 64 + row of each token; negative
+                  slots (padding tokens) and slots past the cache are skipped
+
+    fp8 rows get one scale per 128 latent dims, ``amax / 448``, and e4m3 codes of
+    ``x / scale`` rounded to nearest even -- the layout ``flash_mla_with_kvcache(...,
+    is_fp8_kvcache=True)`` reads.  Runs on the current stream; no host synchronisation.
+    """
+    _require(kv_c.dim() == 2 and kv_c.shape[1] == D_V and kv_c.dtype == torch.bfloat16,
+             "kv_c must be bf16 [num_tokens, 512]")
+    t = kv_c.shape[0]
+    _require(k_pe.dim() == 2 and k_pe.shape == (t, D_QK - D_V) and k_pe.dtype == torch.bfloat16,
+             "k_pe must be bf16 [num_tokens, 64]")
+    _require(kv_c.stride(1) == 1 and k_pe.stride(1) == 1, "kv_c / k_pe rows must be contiguous")
+    _require(kv_c.data_ptr() % 16 == 0 and k_pe.data_ptr() % 16 == 0
+             and kv_c.stride(0) % 8 == 0 and k_pe.stride(0) % 8 == 0,
+             "kv_c / k_pe rows must be 16-byte aligned")
+    _require(kv_cache.dim() == 4 and kv_cache.shape[1] == PAGE_SIZE and kv_cache.shape[2] == 1,
+             "kv_cache must be [num_blocks, 64, 1, row]")
+    if is_fp8_kvcache:
+        _require(kv_cache.dtype in (torch.uint8, torch.float8_e4m3fn)
+                 and kv_cache.shape[3] == FP8_ROW_BYTES, "fp8 kv_cache must be uint8 [.., 656]")
+    else:
+        _require(kv_cache.dtype == torch.bfloat16 and kv_cache.shape[3] == D_QK,
+                 "kv_cache must be bf16 [.., 576]")
+    esz = kv_cache.element_size()
+    _require(kv_cache.stride(3) == 1 and kv_cache.data_ptr() % 16 == 0
+             and (kv_cache.stride(0) * esz) % 16 == 0 and (kv_cache.stride(1) * esz) % 16 == 0,
+             "kv_cache rows must be contiguous and 16-byte aligned")
+    _require(slot_mapping.dim() == 1 and slot_mapping.shape[0] == t
+             and slot_mapping.dtype in (torch.int32, torch.int64),
+             "slot_mapping must be int32 / int64 [num_tokens]")
+    tensors = (kv_c, k_pe, kv_cache, slot_mapping)
+    _require(all(x.is_cuda and x.device == kv_c.device for x in tensors),
+             "all tensors must be CUDA (HIP) tensors on one device")
+    if t == 0:
+        return
+    slots = slot_mapping.to(torch.int64).contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(kv_c.device):
+        _lib.check(lib.fa_mla_kvcache_write(
+            kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0), slots.data_ptr(),
+            t, kv_cache.data_ptr(), kv_cache.stride(0) * esz, kv_cache.stride(1) * esz,
+            kv_cache.shape[0], int(bool(is_fp8_kvcache)), _stream(kv_c.device)))

@@ -170,6 +170,23 @@ int fa_mla_decode_sparse(const fa_mla_decode_args* args, int32_t fp8, void* stre
 int fa_mla_combine(const fa_mla_decode_args* args, void* stream);
 
 /*
+ * KV-cache write path: token i's latent kv_c[i] (512 bf16) and rope k_pe[i]
+ * (64 bf16) go to physical row slot_mapping[i] = page * 64 + row (slots < 0
+ * or past the cache are skipped; with duplicate slots one token wins,
+ * unspecified which).  fp8 == 0: the 1152-byte bf16 row latent | rope.
+ * fp8 != 0: the 656-byte row of fa_mla_decode_sparse(fp8): 512 e4m3 codes,
+ * one fp32 scale per 128 dims (scale = amax / 448, 1 for an all-zero tile,
+ * code = e4m3(clamp(x / scale, +-448)), round to nearest even), 64 bf16 rope.
+ * Strides: kv_c_stride / k_pe_stride in elements, cache strides in bytes.
+ * No counterpart in the reference (it has no cache writer); this is the
+ * producer of the row layouts the MLA decode reads.
+ */
+int fa_mla_kvcache_write(const void* kv_c, int64_t kv_c_stride, const void* k_pe,
+                         int64_t k_pe_stride, const int64_t* slot_mapping, int32_t num_tokens,
+                         void* kv_cache, int64_t kv_block_stride, int64_t kv_row_stride,
+                         int64_t num_kv_blocks, int32_t fp8, void* stream);
+
+/*
  * Workspace bytes one fa_mla_decode_noalloc call with these arguments needs
  * (mode as below), or -1 if the shape fields are invalid.  A call fits when
  * this is <= FA_MLA_NOALLOC_SCRATCH_BYTES.

@@ -133,6 +133,35 @@ def fp8_rows_quantize(latent: torch.Tensor, rope: torch.Tensor,
     return torch.cat([codes, sc, rp], dim=1).reshape(*lead, FP8_ROW_BYTES)
 
 
+def fp8_tile_scales(latent: torch.Tensor) -> torch.Tensor:
+    """Per-128-dim scales of the fp8 row format as the cache writer picks them:
+    ``scale = amax / 448`` in fp32 over each tile of 128 latent dims (so the largest value
+    maps to the largest finite e4m3 code), ``1.0`` for an all-zero tile.  ``latent``
+    ``[..., 512]`` -> scales ``[..., 4]``."""
+    lat = latent.float().reshape(*latent.shape[:-1], 4, 128)
+    amax = lat.abs().amax(dim=-1)
+    return torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+
+
+def kvcache_write_ref(k_cache: torch.Tensor, latent: torch.Tensor, rope: torch.Tensor,
+                      slot_mapping: torch.Tensor, is_fp8: bool) -> torch.Tensor:
+    """A copy of ``k_cache`` with token ``i`` written to physical row ``slot_mapping[i]``
+    (page ``slot // 64``, row ``slot % 64``; slots outside the cache are skipped):
+    bf16 rows ``latent | rope`` (1152 B), or fp8 rows ``fp8_rows_quantize(latent, rope,
+    fp8_tile_scales(latent))`` (656 B)."""
+    out = k_cache.clone()
+    flat = out.view(-1, out.shape[-1])
+    nrows = flat.shape[0]
+    if is_fp8:
+        rows = fp8_rows_quantize(latent.float(), rope, fp8_tile_scales(latent))
+    else:
+        rows = torch.cat([latent, rope], dim=-1).to(out.dtype)
+    for i, slot in enumerate(slot_mapping.tolist()):
+        if 0 <= slot < nrows:
+            flat[slot] = rows[i]
+    return out
+
+
 # --------------------------------------------------------------------------- attention
 
 def attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float,

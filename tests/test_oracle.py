@@ -241,3 +241,42 @@ def test_combine_split_invariance_random_partitions():
 def test_combine_all_empty():
     o, l = orc.combine_ref(torch.zeros((2, 3, 512)), torch.full((2, 3), -math.inf))
     assert torch.equal(o, torch.zeros_like(o)) and bool(torch.isneginf(l).all())
+
+
+# ---------------------------------------------------------------- cache writer
+
+def test_fp8_tile_scales_and_write_ref():
+    """The writer's scale maps each tile's largest magnitude to the largest e4m3 code
+    (0x7E / 0xFE = +-448), an all-zero tile gets scale 1 and zero codes, and the written
+    row decodes to within half an e4m3 step of the input."""
+    gen = torch.Generator().manual_seed(21)
+    lat = torch.randn((5, 512), generator=gen).to(torch.bfloat16)
+    lat[2, 128:256] = 0
+    rope = torch.randn((5, 64), generator=gen).to(torch.bfloat16)
+    sc = orc.fp8_tile_scales(lat)
+    assert sc.shape == (5, 4) and float(sc[2, 1]) == 1.0
+    cache = torch.zeros((1, 64, 1, 656), dtype=torch.uint8)
+    slots = torch.tensor([3, 0, 63, -1, 7])
+    out = orc.kvcache_write_ref(cache, lat, rope, slots, True)
+    flat = out.view(64, 656)
+    for i, s in enumerate(slots.tolist()):
+        if s < 0:
+            continue
+        row = flat[s]
+        codes = row[:512].view(4, 128)
+        for t in range(4):
+            tile = lat[i].float().view(4, 128)[t]
+            if float(tile.abs().max()) > 0:
+                assert int(codes[t, int(tile.abs().argmax())]) & 0x7F == 0x7E
+        dec = orc.fp8_rows_dequant(row.view(1, 656))[0]
+        assert torch.equal(dec[512:], rope[i].float())
+        err = (dec[:512] - lat[i].float()).abs()
+        bound = lat[i].float().abs() * 2.0 ** -4 + sc[i].repeat_interleave(128) * 2.0 ** -10
+        assert bool((err <= bound).all())
+    assert int(flat[1].sum()) == 0  # an unwritten row stays as it was
+    # token 2 (slot 63) has its second tile all zero: codes zero, scale 1
+    assert bool((flat[63][128:256] == 0).all())
+    assert float(flat[63][512:528].view(torch.float32)[1]) == 1.0
+    bf = orc.kvcache_write_ref(torch.zeros((1, 64, 1, 576), dtype=torch.bfloat16), lat, rope,
+                               slots, False)
+    assert torch.equal(bf.view(64, 576)[7], torch.cat([lat[4], rope[4]]))
