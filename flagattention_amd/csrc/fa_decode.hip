@@ -17,7 +17,11 @@
 //   2. O^T += V^T P^T on MFMA 16x16x32 bf16, split by value dims: wave w owns
 //      dims 128w..128w+127 of all 128 rows (256 fp32 accumulators per lane,
 //      in AGPRs).  V^T comes from the tile with transposing LDS reads
-//      (ds_read_b64_tr_b16), P^T from LDS.
+//      (ds_read_b64_tr_b16), P^T from LDS.  The MFMA k order of PV only has to
+//      agree between its two operands, so the 8 tokens of lane group g are
+//      4g..4g+3 and 16+4g..16+4g+3: exactly the S values the softmax lane
+//      holds, so P is stored lane by lane ([row tile][lane][8 bf16]) and both
+//      its writes and its reads are contiguous 1 KB accesses.
 // Splitting PV by dims rather than rows means each wave transposes only its
 // quarter of V: the transposing reads run at about half the rate of plain
 // 16-byte LDS reads, and with a row split every wave would read all of V.
@@ -35,10 +39,12 @@
 //
 // LDS tile layout: the 32 x 72 grid of 16-byte chunks (row r, logical chunk
 // k) is stored as 4 row-groups x 9 chunk-groups of 1 KB blocks.  Block
-// (r/8, k/8) holds slot (r%8)*8 + ((k%8) ^ swz(r)), swz(r) = (r&7)^((r>>3)&1).
-// One wave-wide copy fills exactly one block, so every copy lane has a fixed
-// source offset; the XOR spreads the K operand reads and the V^T transpose
-// reads over the LDS banks.
+// (r/8, k/8) holds slot (r%8)*8 + ((k%8) ^ (r%8)).  One wave-wide copy fills
+// exactly one block, so every copy lane has a fixed source offset.  With this
+// XOR both the K operand reads (ds_read_b128) and the V^T transposing reads
+// in the token order above run without LDS bank conflicts (measured with
+// SQ_LDS_BANK_CONFLICT on gfx950; XOR terms on the row-group, as in
+// (r%8) ^ ((r/8)%2), make the K reads 2-way conflicted).
 //
 // Reference lineage: gather + online softmax of _paged_attn_kernel
 // (src/flag_attn/paged.py:296-337) and the per-split (o, lse) epilogue of
@@ -72,9 +78,10 @@ enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 // kernel, so the compiler can prove that reads of one never alias a copy
 // into another).
 struct __attribute__((aligned(16))) Smem {
-  // P (bf16), row-major [128 rows][32 tokens]; 16-byte chunk c of row r sits
-  // at chunk position c ^ ((r >> 2) & 3).  Between a pass's last PV and the
-  // next P it holds the per-wave second-pass flags, then the row sums.
+  // P (bf16) lane by lane: [row tile][lane][8 tokens], lane l of row tile rt
+  // holding row 16rt + l%16, tokens 4g..4g+3 and 16+4g..16+4g+3 (g = l/16).
+  // Between a pass's last PV and the next P it holds the per-wave second-pass
+  // flags, then the row sums.
   unsigned char p[kRows * 64];
   // Q^T operands that do not fit in VGPRs: [wave][operand][lane]
   bf16x8 qx[4][kQLds][64];
@@ -85,7 +92,7 @@ struct __attribute__((aligned(16))) Smem {
 // zeros.  Never written.
 __device__ __attribute__((aligned(16))) unsigned char g_zero_row[kRowBytes];
 
-__device__ inline int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ inline int swz(int r) { return r & 7; }
 
 // Byte offset of (row r, logical 16-byte chunk k) in a tile.
 __device__ inline int tile_off(int r, int k) {
@@ -296,8 +303,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
   struct LaneOffsets {
     int k[2];   // K operand of QK, by k-step parity
     int v[4];   // V^T operand of PV, by dim tile % 4
-    int pr;     // P^T operand of PV
-    int pw[2];  // P writes of the softmax, by token tile
+    int p;      // P: this lane's 16 bytes of row tile 0 (row tile rt adds rt KB)
   };
   auto lane_offsets = [&]() -> LaneOffsets {
     int ln = lane;
@@ -307,30 +313,32 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // K operand of QK (A of 16x16x32): token 16tt + ii, logical chunk
     // 4kq + g of k-step kq.  Bases by kq parity; kq/2 adds one chunk-group
     // block, tt two row-groups.
-    const int sw = (ii & 7) ^ (ii >> 3);
+    const int sw = ii & 7;
     const int kbase = (ii >> 3) * kRowGroupBytes + 128 * (ii & 7);
 #pragma unroll
     for (int par = 0; par < 2; ++par) o.k[par] = kbase + 16 * ((4 * par + g) ^ sw);
+    return o;
+  };
+  // The V^T and P lane offsets.
+  auto lane_offsets_vp = [&](LaneOffsets& o) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int g = ln >> 4, ii = ln & 15;
     // V^T operand of PV (A of 16x16x32): dim 128*wave + 16dt + ii, tokens
-    // 8g + 0..7.  Two transpose reads of 4 tokens; in the first, lane 4e + q
-    // of each 16-lane group points at token 8g + e, dims 128*wave + 16dt +
-    // 4q..+3.  Offsets by dt % 4 (dt / 4 adds one chunk-group block); the
-    // second read (tokens 8g + 4..7) is the first one of dim tile dt ^ 2
-    // plus 512.
+    // 4g..4g+3 and 16+4g..16+4g+3.  Two transpose reads of 4 tokens; in the
+    // first, lane 4e + q of each 16-lane group points at token 4g + e (row
+    // 4(g%2) + e of row-group g/2), dims 128*wave + 16dt + 4q..+3.  Offsets by
+    // dt % 4 (dt / 4 adds one chunk-group block); the second read (tokens
+    // 16 + 4g + e) is two row-groups further.
     const int e = ii >> 2, qd = ii & 3;
+    const int rr = 4 * (g & 1) + e;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
-      o.v[dt] = (g * kChunkGroups + 2 * wave) * kBlockBytes +
-                16 * (e * 8 + ((2 * dt + (qd >> 1)) ^ e ^ (g & 1))) + 8 * (qd & 1);
-    // P^T operand of PV (B of 16x16x32): row 16rt + ii, tokens 8g..8g+7
-    // (plus rt KB).  The softmax writes row 32*wave + 16rt + ii, tokens
-    // 16tt + 4g..+3 (plus rt KB).
-    const int p_sw = (ii >> 2) & 3;
-    o.pr = ii * 64 + 16 * (g ^ p_sw);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-      o.pw[tt] = (32 * wave + ii) * 64 + 16 * ((2 * tt + (g >> 1)) ^ p_sw) + 8 * (g & 1);
-    return o;
+      o.v[dt] = ((g >> 1) * kChunkGroups + 2 * wave) * kBlockBytes +
+                16 * (rr * 8 + ((2 * dt + (qd >> 1)) ^ rr)) + 8 * (qd & 1);
+    // P: the softmax lane writes (and the PV lane reads) 16 bytes at lane * 16
+    // of its row tile's 1 KB
+    o.p = 16 * ln;
   };
   // Dense copy lane offset inside a half page: row 8*wave + lrow, chunk
   // (lane%8) ^ swz(row) of each 128-byte group (recomputed where used, like
@@ -339,8 +347,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int lr = ln >> 3;
-    return static_cast<unsigned int>((8 * wave + lr) * static_cast<int>(row_stride) +
-                                     16 * ((ln & 7) ^ lr ^ (wave & 1)));
+    // row_stride < 2^24 (checked on the host): a full-rate 24-bit multiply
+    return __umul24(static_cast<unsigned int>(8 * wave + lr),
+                    static_cast<unsigned int>(row_stride)) +
+           static_cast<unsigned int>(16 * ((ln & 7) ^ lr));
   };
 
   // Metadata from another batch / topk must not drive accesses out of bounds:
@@ -458,7 +468,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           src = c.src + 512;
           dst = c.dst + kFp8ScaleOff;
         } else {
-          src = c.src + 528 + 16 * (l8 ^ lrow ^ (wave & 1));
+          src = c.src + 528 + 16 * (l8 ^ lrow);
           dst = c.dst + 8 * kBlockBytes;
         }
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (FA_LDS void*)dst,
@@ -518,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       CopyReq c;
       c.rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
       c.src = row_ptr(__shfl(r, 8 * wave + lrow));
-      if constexpr (kMode == kSparseBf16) c.src += 16 * ((lane & 7) ^ lrow ^ (wave & 1));
+      if constexpr (kMode == kSparseBf16) c.src += 16 * ((lane & 7) ^ lrow);
       c.voff = 0;
       c.dst = buf + wave * kRowGroupBytes;
       return c;
@@ -540,7 +550,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     auto v_read = [&](const LaneOffsets& lo, const unsigned char* kb, int dt) -> bf16x8 {
       const unsigned char* p = kb + (dt >> 2) * kBlockBytes;
       const bf16x4 l4 = lds_read_tr4(p + lo.v[dt & 3]);
-      const bf16x4 h4 = lds_read_tr4(p + lo.v[(dt & 3) ^ 2] + 512);
+      const bf16x4 h4 = lds_read_tr4(p + lo.v[dt & 3] + 2 * kRowGroupBytes);
       return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
@@ -613,7 +623,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         }
         barrier();
         const unsigned int vm = vq[0];
-        const LaneOffsets lo = lane_offsets();
+        LaneOffsets lo = lane_offsets();
+        lane_offsets_vp(lo);
         CopyReq creq;  // tile t+2, issued block by block during QK(t) or PV(t)
         if constexpr (kMode == kDense) {
           unsigned int m;
@@ -737,13 +748,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           for (int rt = 0; rt < 2; ++rt) {
             lsum[rt] += ((sv[rt][0] + sv[rt][1]) + (sv[rt][2] + sv[rt][3])) +
                         ((sv[rt][4] + sv[rt][5]) + (sv[rt][6] + sv[rt][7]));
+            uintx4 w;
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-              uintx2 w;
-              w[0] = pack_bf16x2(sv[rt][4 * tt + 0], sv[rt][4 * tt + 1]);
-              w[1] = pack_bf16x2(sv[rt][4 * tt + 2], sv[rt][4 * tt + 3]);
-              *reinterpret_cast<uintx2*>(sm.p + lo.pw[tt] + rt * 1024) = w;
-            }
+            for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(sv[rt][2 * j], sv[rt][2 * j + 1]);
+            *reinterpret_cast<uintx4*>(sm.p + lo.p + (2 * wave + rt) * 1024) = w;
           }
         }
 #pragma unroll
@@ -785,13 +793,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             ps += sv[i];
           }
           lsum[rt] += ps;
+          uintx4 w;
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            uintx2 w;
-            w[0] = pack_bf16x2(sv[4 * tt + 0], sv[4 * tt + 1]);
-            w[1] = pack_bf16x2(sv[4 * tt + 2], sv[4 * tt + 3]);
-            *reinterpret_cast<uintx2*>(sm.p + lo.pw[tt] + rt * 1024) = w;
-          }
+          for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(sv[2 * j], sv[2 * j + 1]);
+          *reinterpret_cast<uintx4*>(sm.p + lo.p + (2 * wave + rt) * 1024) = w;
         }
         barrier();
 
@@ -802,7 +807,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           for (int dt = kVPre; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
           bf16x8 pb[2];
           auto p_read = [&](int rt) -> bf16x8 {
-            return *reinterpret_cast<const bf16x8*>(sm.p + lo.pr + rt * 1024);
+            return *reinterpret_cast<const bf16x8*>(sm.p + lo.p + rt * 1024);
           };
           pb[0] = p_read(0);
           static_for<kRowTiles>([&](auto rtt) {
@@ -994,8 +999,8 @@ int check_common(const fa_mla_decode_args* a) {
   FA_CHECK_ARG((reinterpret_cast<uintptr_t>(a->kv) & 15) == 0 && (a->kv_block_stride % 16) == 0 &&
                    (a->kv_row_stride % 16) == 0,
                "kv cache rows must be 16-byte aligned");
-  FA_CHECK_ARG(a->kv_row_stride > 0 && a->kv_row_stride <= (1 << 24),
-               "kv_row_stride %lld outside (0, 2^24]", static_cast<long long>(a->kv_row_stride));
+  FA_CHECK_ARG(a->kv_row_stride > 0 && a->kv_row_stride < (1 << 24),
+               "kv_row_stride %lld outside (0, 2^24)", static_cast<long long>(a->kv_row_stride));
   return FA_OK;
 }
 
