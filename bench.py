@@ -1,6 +1,7 @@
 """MLA decode benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload dense|skew|sparse|sparse_fp8]
+    python bench.py --workload gqa_paged|gqa_splitkv|topk       # the other decode-path kernels
     python bench.py --traffic-calibrate [--workload ...]   # driver for rocprofv3 --pmc passes
 
 A step is one decode of the whole batch through the public path: scheduler metadata
@@ -348,13 +349,98 @@ def gqa_cpu_baseline(spec, inputs, scale) -> dict:
                                       f"scaled x{b} to the full step"}
 
 
+# Top-k index producer workload (flag_attn.topk_indices): the index shape of the fp8 sparse
+# benchmark -- 128 sequences, one query token, 65536 indexer scores each, top-2048.
+TOPK_WORKLOADS = {
+    "topk": dict(name="topk_b128_len65536_top2048", batch=128, s_q=1, length=65536,
+                 topk=2048, seed=13),
+}
+TOPK_METRIC = "top-k index producer µs/step + achieved HBM GB/s (% of roofline)"
+
+
+def run_topk(args) -> None:
+    """Index producer bench: fp32 scores resident in HBM (two copies rotated); a step is
+    one flag_attn.topk_indices launch, timed with events around it on its stream."""
+    import flag_attn
+
+    spec = TOPK_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(spec["seed"])
+    b, s_q, length, topk = spec["batch"], spec["s_q"], spec["length"], spec["topk"]
+    scores = [torch.randn((b, s_q, length), generator=gen, device=dev) for _ in range(2)]
+    lens = torch.full((b,), length, dtype=torch.int32, device=dev)
+    out = torch.empty((b, s_q, topk), dtype=torch.int32, device=dev)
+
+    def step(i):
+        return flag_attn.topk_indices(scores[i % 2], lens, topk, out=out)
+
+    t_warm = time.perf_counter()
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    settle_steps = 0
+    while time.perf_counter() - t_warm < SETTLE_S:
+        for _ in range(20):
+            step(settle_steps)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_warm
+    every = max(1, min(EVENT_EVERY, args.steps // MIN_EVENT_LAUNCHES))
+    stream = torch.cuda.current_stream()
+    evs = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for i in range(0, args.steps, every)}
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev = evs.get(i)
+        if ev:
+            ev[0].record(stream)
+        step(i)
+        if ev:
+            ev[1].record(stream)
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) / args.steps * 1e6
+    dec = sorted(s.elapsed_time(e) for s, e in evs.values())
+    k_us = sum(dec) / len(dec) * 1e3
+    nbytes = b * s_q * (length * 4 + topk * 4) + b * 4
+    gbs = nbytes / (k_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import topk_oracle as tko
+        rows = 8
+        sample = scores[0][:rows].cpu().numpy()
+        lens_cpu = [length] * rows
+        tko.topk_indices_ref(sample[:1], lens_cpu[:1], topk)
+        t1 = time.perf_counter()
+        tko.topk_indices_ref(sample, lens_cpu, topk)
+        t_cpu = time.perf_counter() - t1
+        cpu = {"value": round(t_cpu * (b * s_q / rows) * 1e6, 1), "unit": "µs/step", "cores": 1,
+               "kind": "port", "sample": f"{rows} of {b * s_q} rows (numpy lexsort), scaled "
+                                         f"x{b * s_q // rows} to the full step"}
+    rec = {
+        "metric": TOPK_METRIC, "value": round(us_step, 2), "unit": "µs/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "settle_s": round(settle_s, 3),
+        "settle_steps": settle_steps, "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": spec["name"], "batch": b, "s_q": s_q, "length": length,
+                   "topk": topk},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "topk_indices_kernel", "kernel_launches_timed": len(dec),
+                     "kernel_us_mean": round(k_us, 2), "bytes_per_launch": nbytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--workload", default="dense",
-                    choices=["dense", "skew", "sparse", "sparse_fp8"] + list(GQA_WORKLOADS))
+                    choices=["dense", "skew", "sparse", "sparse_fp8"] + list(GQA_WORKLOADS)
+                    + list(TOPK_WORKLOADS))
     ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-calibrate", action="store_true",
@@ -370,6 +456,9 @@ def main() -> None:
 
     if args.workload in GQA_WORKLOADS:
         run_gqa(args)
+        return
+    if args.workload in TOPK_WORKLOADS:
+        run_topk(args)
         return
 
     import flag_attn.mla as fa

@@ -8,6 +8,8 @@ exports the decode operators built for MI355X:
 * ``get_mla_metadata`` / ``flash_mla_with_kvcache`` -- MLA decode (dense and sparse top-k
   over the paged latent KV cache, split-KV scheduling, LSE combine);
 * ``concat_and_cache_mla`` -- the cache write path of those layouts (bf16 and fp8 rows);
+* ``topk_indices`` -- the index producer of sparse decode (top-k positions per query token
+  from per-key indexer scores);
 * ``paged_attention`` -- MHA / GQA decode over a paged KV cache (``paged.py:20-177``);
 * ``flash_attention_split_kv`` -- flash decoding over contiguous K/V (``split_kv.py:280-344``);
 * ``flash_attention`` -- the forward of ``flash.py:269-300`` through its split-KV decode
@@ -22,11 +24,13 @@ from flag_attn.mla import (  # noqa: F401
     concat_and_cache_mla,
     flash_mla_with_kvcache,
     get_mla_metadata,
+    topk_indices,
 )
 from flag_attn.paged import attention as paged_attention  # noqa: F401
 from flag_attn.split_kv import attention as flash_attention_split_kv  # noqa: F401
 from flag_attn.flash import attention as flash_attention  # noqa: F401
 
-__all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "concat_and_cache_mla", "paged_attention",
+__all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "concat_and_cache_mla", "topk_indices",
+           "paged_attention",
            "flash_attention_split_kv", "flash_attention"]
 __version__ = "0.2.0"

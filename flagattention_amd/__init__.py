@@ -12,11 +12,14 @@ from .mla import (  # noqa: F401
     DecodeWorkspace,
     MLAArgumentError,
     flash_mla_with_kvcache,
+    concat_and_cache_mla,
     get_mla_metadata,
     sparse_rows,
+    topk_indices,
 )
 
-__all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "sparse_rows", "DecodeWorkspace",
+__all__ = ["get_mla_metadata", "flash_mla_with_kvcache", "concat_and_cache_mla", "topk_indices",
+           "sparse_rows", "DecodeWorkspace",
            "MLAArgumentError", "ArgumentError", "paged_attention", "flash_attention_split_kv",
            "flash_attention"]
 __version__ = "0.1.0"

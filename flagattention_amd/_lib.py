@@ -118,6 +118,11 @@ SIGNATURES = {
         [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
          ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
          ctypes.c_int32, ctypes.c_void_p]),
+    "fa_mla_topk_indices": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
+         ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+         ctypes.c_void_p]),
     "fa_gqa_decode_args_size": (ctypes.c_int64, []),
     "fa_gqa_decode": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),
     "fa_gqa_combine": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),

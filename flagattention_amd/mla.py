@@ -506,3 +506,59 @@ def concat_and_cache_mla(
             kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0), slots.data_ptr(),
             t, kv_cache.data_ptr(), kv_cache.stride(0) * esz, kv_cache.stride(1) * esz,
             kv_cache.shape[0], int(bool(is_fp8_kvcache)), _stream(kv_c.device)))
+
+
+TOPK_MAX_LEN = 65536
+TOPK_MAX_K = 65536
+
+
+def topk_indices(
+    scores: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    topk: int,
+    causal: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Sparse-attention indices from per-key indexer scores.
+
+    scores         fp32 [B, s_q, L]: score of key position l for query token t of
+                   sequence b (last dim contiguous); L <= 65536
+    cache_seqlens  int32 [B]
+    topk           1..65536
+    causal         query token t sees keys [0, cache_seqlens[b] - (s_q - 1 - t)) (bottom-
+                   right aligned, as the dense decode's causal mask); else [0, cache_seqlens[b])
+    out            optional int32 [B, s_q, topk] contiguous to write into
+
+    Returns int32 [B, s_q, topk]: the positions of the min(topk, n) largest visible
+    scores in ascending order, then -1 -- the ``indices`` argument of
+    ``flash_mla_with_kvcache``.  Scores compare by the total order of their bit patterns
+    (-NaN < -inf < -0 < +0 < +inf < +NaN), ties by lower position, so the result is
+    deterministic.  Runs on the current stream; no host synchronisation.
+    """
+    _require(isinstance(scores, torch.Tensor) and scores.dim() == 3
+             and scores.dtype == torch.float32, "scores must be float32 [batch, s_q, len]")
+    batch, s_q, length = scores.shape
+    _require(length <= TOPK_MAX_LEN, f"scores length {length} > {TOPK_MAX_LEN}")
+    _require(isinstance(topk, int) and 1 <= topk <= TOPK_MAX_K,
+             f"topk must be an int in [1, {TOPK_MAX_K}]")
+    _require(scores.stride(2) == 1 or length <= 1, "scores last dim must be contiguous")
+    _require(isinstance(cache_seqlens, torch.Tensor) and cache_seqlens.dtype == torch.int32
+             and cache_seqlens.shape == (batch,), "cache_seqlens must be int32 [batch]")
+    tensors = [scores, cache_seqlens]
+    if out is None:
+        out = torch.empty((batch, s_q, topk), dtype=torch.int32, device=scores.device)
+    else:
+        _require(out.dtype == torch.int32 and out.shape == (batch, s_q, topk)
+                 and out.is_contiguous(), "out must be contiguous int32 [batch, s_q, topk]")
+        tensors.append(out)
+    _require(all(x.is_cuda and x.device == scores.device for x in tensors),
+             "all tensors must be CUDA (HIP) tensors on one device")
+    if batch == 0:
+        return out
+    seqlens = cache_seqlens.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(scores.device):
+        _lib.check(lib.fa_mla_topk_indices(
+            scores.data_ptr(), scores.stride(0), scores.stride(1), seqlens.data_ptr(), batch, s_q,
+            length, topk, int(bool(causal)), out.data_ptr(), _stream(scores.device)))
+    return out

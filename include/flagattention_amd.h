@@ -43,6 +43,8 @@ extern "C" {
 /* Workspace of fa_mla_decode_noalloc: one file-scope device array of this
  * many bytes per device the library runs on, held until the process ends. */
 #define FA_MLA_NOALLOC_SCRATCH_BYTES (64ll << 20)
+#define FA_TOPK_MAX_LEN 65536 /* scores per row fa_mla_topk_indices takes */
+#define FA_TOPK_MAX_K 65536   /* largest topk it produces                 */
 
 /* Version of this ABI (FA_ABI_VERSION of the built library). */
 int fa_abi_version(void);
@@ -185,6 +187,23 @@ int fa_mla_kvcache_write(const void* kv_c, int64_t kv_c_stride, const void* k_pe
                          int64_t k_pe_stride, const int64_t* slot_mapping, int32_t num_tokens,
                          void* kv_cache, int64_t kv_block_stride, int64_t kv_row_stride,
                          int64_t num_kv_blocks, int32_t fp8, void* stream);
+
+/*
+ * Top-k index producer: the indices tensor of fa_mla_decode_sparse from
+ * per-key indexer scores.  scores: fp32 [batch, s_q, len] (last dim
+ * contiguous, strides stride_b / stride_t in elements); query token t of
+ * sequence b sees keys [0, n) with n = cache_seqlens[b] - (causal ? s_q-1-t : 0),
+ * clipped to [0, len).  indices: int32 [batch, s_q, topk] contiguous, the
+ * positions of the min(topk, n) largest visible scores in ascending order,
+ * then -1.  Scores compare by the total order of their bit patterns
+ * (-NaN < -inf < -0 < +0 < +inf < +NaN), ties by lower position.  Limits:
+ * len <= FA_TOPK_MAX_LEN, 1 <= topk <= FA_TOPK_MAX_K.
+ * No counterpart in the reference (it has no sparse path); this produces the
+ * index format the sparse decode consumes.
+ */
+int fa_mla_topk_indices(const float* scores, int64_t stride_b, int64_t stride_t,
+                        const int32_t* cache_seqlens, int32_t batch, int32_t s_q, int32_t len,
+                        int32_t topk, int32_t causal, int32_t* indices, void* stream);
 
 /*
  * Workspace bytes one fa_mla_decode_noalloc call with these arguments needs

@@ -126,3 +126,25 @@ def test_flag_attn_namespace_exports_the_mla_operators():
                          "tile_scheduler_metadata", "num_splits", "softmax_scale", "causal",
                          "is_fp8_kvcache", "indices"]
     assert dec["indices"].default is None and dec["causal"].default is False
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(scores=torch.zeros(2, 1, 10, dtype=torch.float16)), "float32"),
+    (dict(scores=torch.zeros(2, 10)), "float32"),
+    (dict(scores=torch.zeros(2, 1, 65537)), "length"),
+    (dict(topk=0), "topk"),
+    (dict(topk=65537), "topk"),
+    (dict(cache_seqlens=torch.zeros(3, dtype=torch.int32)), "cache_seqlens"),
+    (dict(cache_seqlens=torch.zeros(2, dtype=torch.int64)), "cache_seqlens"),
+    (dict(scores=torch.zeros(2, 1, 20)[:, :, ::2]), "contiguous"),
+    (dict(out=torch.zeros(2, 1, 8, dtype=torch.int64)), "out"),
+    (dict(), "CUDA"),
+])
+def test_topk_indices_rejects(kw, msg):
+    args = dict(scores=torch.zeros(2, 1, 10), cache_seqlens=torch.zeros(2, dtype=torch.int32),
+                topk=8)
+    args.update(kw)
+    with pytest.raises(MLAArgumentError, match=msg):
+        fa.topk_indices(**args)
+    import flag_attn
+    assert flag_attn.topk_indices is fa.topk_indices
