@@ -147,16 +147,20 @@ def algorithmic_work(spec, lens_cpu, indices) -> tuple:
     return nbytes, flops
 
 
+# The sources the MLA decode kernel is compiled from (its translation unit and the
+# headers it includes); a traffic record holds only while these are unchanged.
+DECODE_SOURCES = ("flagattention_amd/csrc/fa_decode.hip", "flagattention_amd/csrc/fa_common.h",
+                  "flagattention_amd/csrc/fa_wave.h", "include/flagattention_amd.h")
+
+
 def kernel_sources_sha() -> str:
-    """sha256 (16 hex) over the HIP sources and C header, as recorded in profiles/."""
+    """sha256 (16 hex) over the decode kernel's sources, as recorded in profiles/."""
     import hashlib
     h = hashlib.sha256()
-    for d in (os.path.join(ROOT, "flagattention_amd", "csrc"), os.path.join(ROOT, "include")):
-        for f in sorted(os.listdir(d)):
-            if f.endswith((".hip", ".h")):
-                h.update(f.encode())
-                with open(os.path.join(d, f), "rb") as fh:
-                    h.update(fh.read())
+    for rel in DECODE_SOURCES:
+        h.update(rel.encode())
+        with open(os.path.join(ROOT, rel), "rb") as fh:
+            h.update(fh.read())
     return h.hexdigest()[:16]
 
 
