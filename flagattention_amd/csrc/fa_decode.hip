@@ -191,12 +191,18 @@ __device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
   const int r = lane >> 3, e = lane & 7;  // row r of the group, codes 64e..64e+63
   const unsigned char* rg = buf + wave * kRowGroupBytes;
   const unsigned char* src = rg + 1024 * (e >> 1) + 16 * (8 * r + 4 * (e & 1));
+  // Lane (r, e) takes its four 16-code pieces in the order m = (i + e/2) % 4: the
+  // reads of one instruction then fall in 16 different bank groups per 16 lanes, and
+  // its writes in 8 (2-way) instead of 2 (8-way).
+  const int rot = e >> 1;
   uintx4 code[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) code[i] = *reinterpret_cast<const uintx4*>(src + 16 * i);
+  for (int i = 0; i < 4; ++i)
+    code[i] = *reinterpret_cast<const uintx4*>(src + 16 * ((i + rot) & 3));
   const float scale = *reinterpret_cast<const float*>(rg + kFp8ScaleOff + 128 * r + 4 * (e >> 1));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const int m = (i + rot) & 3;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {  // 8 codes -> 8 bf16 = one 16-byte chunk
       const unsigned int w0 = code[i][2 * h], w1 = code[i][2 * h + 1];
@@ -207,7 +213,7 @@ __device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
       o[1] = pack_bf16x2(b[0] * scale, b[1] * scale);
       o[2] = pack_bf16x2(c[0] * scale, c[1] * scale);
       o[3] = pack_bf16x2(d[0] * scale, d[1] * scale);
-      *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * i + h)) = o;
+      *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * m + h)) = o;
     }
   }
 }
