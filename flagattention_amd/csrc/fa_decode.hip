@@ -301,6 +301,14 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 
   const unsigned char* kv = static_cast<const unsigned char*>(a.kv);
   const bf16* q = static_cast<const bf16*>(a.q);
+  // The zero row's address, taken once into scalars the compiler cannot see
+  // through: left to itself it reloads the address from the GOT in every step.
+  const unsigned char* const zero_row = [] {
+    const unsigned long long v = reinterpret_cast<unsigned long long>(g_zero_row);
+    unsigned int lo = static_cast<unsigned int>(v), hi = static_cast<unsigned int>(v >> 32);
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return reinterpret_cast<const unsigned char*>((static_cast<unsigned long long>(hi) << 32) | lo);
+  }();
 
   // ---- per-lane LDS offsets ----
   // Recomputed at every step from a lane index the compiler cannot see
@@ -413,7 +421,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         const bf16* qrow =
             map_row(32 * wave + 16 * rt + (ln & 15), s, hh)
                 ? q + b * a.q_stride_b + s * a.q_stride_s + hh * a.q_stride_h + 8 * (ln >> 4)
-                : reinterpret_cast<const bf16*>(g_zero_row);
+                : reinterpret_cast<const bf16*>(zero_row);
 #pragma unroll
         for (int kq = 0; kq < kQkSteps; ++kq) {
           const int j = 2 * kq + rt;
@@ -509,37 +517,49 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       *mask = nrows >= kTileRows ? ~0u : ((1u << nrows) - 1u);
       return c;
     };
-    // sparse: physical row of tile row (lane % 32) of tile u (-1: masked)
-    // sparse: physical row of tile row (lane % 32) of tile u, as loaded
-    // (the tile index is clamped so the load stays inside the row list);
-    // row_valid masks tiles past the end (-1: masked).  The select waits for
-    // the load, so it is applied only where the row is used.
-    auto load_row = [&](int u) -> int32_t {
-      const int uu = u < ntiles ? u : ntiles - 1;
-      return srows[(tok_lo + kTileRows * uu) + (lane & 31)];
+    // sparse: physical rows of tile u, as loaded, twice: m = tile row
+    // (lane % 32), the key-mask layout; g = tile row 8*wave + lane/8, the row
+    // this lane copies (two loads instead of a lane exchange that would wait
+    // on the LDS queue).  The tile index is clamped so the loads stay inside
+    // the row list; row_valid masks tiles past the end (-1: masked).  The
+    // select waits for the loads, so it is applied only where the rows are used.
+    struct RowPair {
+      int32_t m, g;
     };
-    auto row_valid = [&](int u, int32_t r) -> int32_t { return u < ntiles ? r : -1; };
+    auto load_row = [&](int u) -> RowPair {
+      const int uu = u < ntiles ? u : ntiles - 1;
+      const int32_t* base = srows + tok_lo + kTileRows * uu;
+      return RowPair{base[lane & 31], base[8 * wave + lrow]};
+    };
+    auto row_valid = [&](int u, RowPair r) -> RowPair {
+      return u < ntiles ? r : RowPair{-1, -1};
+    };
+    // block_stride < 2^32 and row_stride < 2^24 (checked on the host): one
+    // 32x32->64-bit multiply-add and a 24-bit multiply, no branch
     auto row_ptr = [&](int32_t r) -> const unsigned char* {
-      return r >= 0 ? kv + static_cast<long long>(r >> 6) * block_stride +
-                          static_cast<long long>(r & 63) * row_stride
-                    : static_cast<const unsigned char*>(g_zero_row);
+      const unsigned int rr = static_cast<unsigned int>(r < 0 ? 0 : r);
+      const unsigned char* p =
+          kv + static_cast<unsigned long long>(rr >> 6) * static_cast<unsigned int>(block_stride) +
+          __umul24(rr & 63u, static_cast<unsigned int>(row_stride));
+      return r >= 0 ? p : zero_row;
     };
     // sparse: key mask of a tile from its rows (lanes 0..31 hold rows 0..31)
-    auto row_mask = [&](int32_t r) -> unsigned int {
-      return static_cast<unsigned int>(__ballot(r >= 0));
+    auto row_mask = [&](RowPair r) -> unsigned int {
+      return static_cast<unsigned int>(__ballot(r.m >= 0));
     };
     // sparse: gathered rows (r = the rows of lanes 0..31); bf16: this lane's
     // chunk of its row, fp8: its row (the copies add their offsets)
-    auto gather_req = [&](int32_t r, unsigned char* buf) -> CopyReq {
+    auto gather_req = [&](RowPair r, unsigned char* buf) -> CopyReq {
       CopyReq c;
-      c.rs = __builtin_amdgcn_make_buffer_rsrc(g_zero_row, 0, 0, 0x00020000);  // unused
-      c.src = row_ptr(__shfl(r, 8 * wave + lrow));
+      c.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(zero_row), 0, 0,
+                                               0x00020000);  // unused
+      c.src = row_ptr(r.g);
       if constexpr (kMode == kSparseBf16) c.src += 16 * ((lane & 7) ^ lrow);
       c.voff = 0;
       c.dst = buf + wave * kRowGroupBytes;
       return c;
     };
-    int32_t rq0 = -1, rq1 = -1;  // sparse: rows of tiles t+2 and t+3
+    RowPair rq0{-1, -1}, rq1{-1, -1};  // sparse: rows of tiles t+2 and t+3
     // key masks of tiles t, t+1 (scalar queue; bit j: token j of the tile)
     unsigned int vq[2] = {0u, 0u};
 
@@ -569,9 +589,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         copy_all(dense_req(1, kv_buf1, &vq[1]));
         prefetch_page(2);
       } else {
-        const int32_t r0l = load_row(0), r1l = load_row(1);
+        const RowPair r0l = load_row(0), r1l = load_row(1);
         wait_vmem<0>();
-        const int32_t r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
+        const RowPair r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
         vq[0] = row_mask(r0);
         vq[1] = row_mask(r1);
         // issue order copies(0), rows(2), copies(1), rows(3): the order the
@@ -623,7 +643,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         if constexpr (kMode == kSparseFp8) {
           wait_vmem<0>();
         } else if constexpr (kMode == kSparseBf16) {
-          wait_vmem<kCopiesPerWave + 1>();  // also the rows of tile t+2
+          wait_vmem<kCopiesPerWave + 2>();  // also the rows of tile t+2 (two loads)
         } else {
           wait_vmem<kCopiesPerWave>();
         }
@@ -638,7 +658,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           vq[0] = vq[1];
           vq[1] = m;
         } else if constexpr (kMode == kSparseBf16) {
-          const int32_t r = row_valid(t + 2, rq0);
+          const RowPair r = row_valid(t + 2, rq0);
           rq0 = rq1;
           rq1 = load_row(t + 4);  // before the copies: a later wait covers it
           creq = gather_req(r, b_cp);
@@ -650,7 +670,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           // (Converting it at the end of this step instead, which gives its
           // copies half a step more, measured 1.7% slower.)
           dequant_fp8_rowgroup(FA_KVBUF((K + 1) % 3), wave);
-          const int32_t r = row_valid(t + 2, rq0);
+          const RowPair r = row_valid(t + 2, rq0);
           rq0 = rq1;
           rq1 = load_row(t + 4);
           creq = gather_req(r, b_cp);
@@ -1007,6 +1027,8 @@ int check_common(const fa_mla_decode_args* a) {
                "kv cache rows must be 16-byte aligned");
   FA_CHECK_ARG(a->kv_row_stride > 0 && a->kv_row_stride < (1 << 24),
                "kv_row_stride %lld outside (0, 2^24)", static_cast<long long>(a->kv_row_stride));
+  FA_CHECK_ARG(a->kv_block_stride > 0 && a->kv_block_stride < (1ll << 32),
+               "kv_block_stride %lld outside (0, 2^32)", static_cast<long long>(a->kv_block_stride));
   return FA_OK;
 }
 
