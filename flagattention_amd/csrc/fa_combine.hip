@@ -10,11 +10,13 @@
 // One 64-lane wave per (sequence, query row); each lane owns 8 of the 512
 // value dims, so a bf16 partial row is one 16-byte load per lane (partials
 // are stored in bf16: the combine and the decode epilogue move half the
-// bytes, and the weighted sum is accumulated in fp32).  The split lse values
-// are loaded one per lane and reduced across the wave, and the partial rows
-// are loaded four at a time, so a row costs three dependent memory round
-// trips whatever its split count (up to 64 splits; more take one extra pass
-// per 64).
+// bytes, and the weighted sum is accumulated in fp32).  Up to 8 splits (the
+// usual case at the default part counts) every lane loads every split's
+// lse (one address per split: a broadcast) beside the partial rows and
+// reduces them itself -- one memory round trip and no cross-lane traffic.
+// More splits: the lse values are loaded one per lane and reduced across the
+// wave, and the partial rows are loaded four at a time (three dependent round
+// trips; more than 64 splits take one extra pass per 64).
 #include "fa_common.h"
 
 namespace fa {
@@ -33,6 +35,51 @@ __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
   return v;
+}
+
+// Rows with 1 < ns <= N splits: all loads issued at once (split indices past
+// ns repeat the last split and weigh nothing), then a lane-local reduction.
+template <int N>
+__device__ __attribute__((always_inline)) inline void combine_small(const bf16* orows, const float* lrow, int ns, int rows,
+                                     bf16* orow, float* lse_out, int lane) {
+  const float ninf = -__builtin_inff();
+  float lv[N];
+  bf16x8 ov[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const long long ii = i < ns ? i : ns - 1;
+    lv[i] = lrow[ii * rows];
+    ov[i] = *reinterpret_cast<const bf16x8*>(orows + ii * rows * kDv);
+  }
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < N; ++i) mx = i < ns ? fmaxf(mx, lv[i]) : mx;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  float total = ninf;
+  if (mx != ninf) {
+    float w[N];
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      w[i] = (i < ns && lv[i] != ninf) ? expf(lv[i] - mx) : 0.f;
+      sum += w[i];
+    }
+    total = mx + logf(sum);
+    const float inv = 1.f / sum;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const float wi = w[i] * inv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wi * static_cast<float>(ov[i][e]);
+    }
+  }
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = static_cast<bf16>(acc[e]);
+  *reinterpret_cast<bf16x8*>(orow) = v;
+  if (lane == 0) *lse_out = total;
 }
 
 __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
@@ -55,6 +102,14 @@ __global__ __launch_bounds__(kCombineThreads) void mla_combine_kernel(
   const float ninf = -__builtin_inff();
   const float* lrow = lse_accum + static_cast<long long>(s0) * rows + row;  // stride rows
   const bf16* orows = o_accum + (static_cast<long long>(s0) * rows + row) * kDv + lane * 8;
+  if (ns > 1 && ns <= 8) {  // uniform
+    if (ns <= 4) {
+      combine_small<4>(orows, lrow, ns, rows, orow, lse_out, lane);
+    } else {
+      combine_small<8>(orows, lrow, ns, rows, orow, lse_out, lane);
+    }
+    return;
+  }
 
   // lane i holds the lse of split c + i of chunk c (64 splits per chunk).
   // The first kUnroll partial rows do not depend on the lse: they are loaded
