@@ -9,7 +9,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflagattention_amd.so")
 
 FA_OK = 0
@@ -122,7 +122,9 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
          ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
-         ctypes.c_void_p]),
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
+    "fa_mla_topk_workspace_bytes": (
+        ctypes.c_int64, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
     "fa_gqa_decode_args_size": (ctypes.c_int64, []),
     "fa_gqa_decode": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),
     "fa_gqa_combine": (ctypes.c_int, [ctypes.POINTER(GqaArgs), ctypes.c_void_p]),

@@ -557,8 +557,13 @@ def topk_indices(
         return out
     seqlens = cache_seqlens.contiguous()
     lib = _lib.load()
+    ws_bytes = int(lib.fa_mla_topk_workspace_bytes(batch, s_q, length, topk))
+    _require(ws_bytes >= 0, "invalid top-k shape")
+    ws = (torch.empty(ws_bytes, dtype=torch.uint8, device=scores.device) if ws_bytes > 0
+          else None)
     with torch.cuda.device(scores.device):
         _lib.check(lib.fa_mla_topk_indices(
             scores.data_ptr(), scores.stride(0), scores.stride(1), seqlens.data_ptr(), batch, s_q,
-            length, topk, int(bool(causal)), out.data_ptr(), _stream(scores.device)))
+            length, topk, int(bool(causal)), out.data_ptr(), _ptr(ws), ws_bytes,
+            _stream(scores.device)))
     return out

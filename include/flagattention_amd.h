@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 #define FA_OK 0
 #define FA_ERR_INVALID_ARG (-1) /* shape / size / pointer check failed   */
@@ -197,13 +197,19 @@ int fa_mla_kvcache_write(const void* kv_c, int64_t kv_c_stride, const void* k_pe
  * positions of the min(topk, n) largest visible scores in ascending order,
  * then -1.  Scores compare by the total order of their bit patterns
  * (-NaN < -inf < -0 < +0 < +inf < +NaN), ties by lower position.  Limits:
- * len <= FA_TOPK_MAX_LEN, 1 <= topk <= FA_TOPK_MAX_K.
+ * len <= FA_TOPK_MAX_LEN, 1 <= topk <= FA_TOPK_MAX_K.  workspace (4-byte
+ * aligned, workspace_bytes long, may be NULL) lets long rows run in two
+ * stages (chunk candidates, then a merge); the result is the same either way.
  * No counterpart in the reference (it has no sparse path); this produces the
  * index format the sparse decode consumes.
  */
 int fa_mla_topk_indices(const float* scores, int64_t stride_b, int64_t stride_t,
                         const int32_t* cache_seqlens, int32_t batch, int32_t s_q, int32_t len,
-                        int32_t topk, int32_t causal, int32_t* indices, void* stream);
+                        int32_t topk, int32_t causal, int32_t* indices, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes fa_mla_topk_indices uses for this shape (0: one stage), -1 if invalid. */
+int64_t fa_mla_topk_workspace_bytes(int32_t batch, int32_t s_q, int32_t len, int32_t topk);
 
 /*
  * Workspace bytes one fa_mla_decode_noalloc call with these arguments needs

@@ -66,6 +66,32 @@ def test_ties_and_specials(topk, kind):
     _run(scores, [12000, 9000], topk, causal=kind != "const")
 
 
+@pytest.mark.parametrize("kind", ["int", "const", "specials"])
+def test_two_stage_ties_and_specials(kind):
+    """Rows long enough for the chunked two-stage path (50000 scores, top-1000): ties
+    that span chunks, constant rows, IEEE specials."""
+    gen = torch.Generator().manual_seed(7)
+    shape = (2, 2, 50000)
+    if kind == "int":
+        scores = torch.randint(-3, 3, shape, generator=gen).float()
+    elif kind == "const":
+        scores = torch.full(shape, 0.25)
+    else:
+        pool = np.array([0xFFFFFFFF, 0xFF800000, 0x80000000, 0x00000000, 0x3F800000,
+                         0x7F800000, 0x7FC00000], np.uint32)
+        pick = torch.randint(0, pool.size, shape, generator=gen).numpy()
+        scores = torch.from_numpy(pool[pick].view(np.float32).copy())
+    _run(scores, [50000, 33000], 1000, causal=True)
+
+
+def test_two_stage_chunk_boundaries():
+    """Sequence lengths that end inside, at, and just past chunk boundaries, and chunks
+    with fewer scores than topk."""
+    gen = torch.Generator().manual_seed(8)
+    scores = torch.randn((6, 1, 65536), generator=gen)
+    _run(scores, [16384, 16385, 2049, 32768 + 2047, 49152 + 5000, 65536], 2048, causal=False)
+
+
 def test_all_ones_pattern_rows():
     """Every score is the bit pattern 0xFFFFFFFF (key 0, the same key the kernel's padding
     slots carry): ties resolve by position over the visible keys only."""
