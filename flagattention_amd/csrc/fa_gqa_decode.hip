@@ -72,14 +72,20 @@ __device__ inline int vswz(int r) {
   return H > 1 ? 2 * ((r / L) % H) : 0;
 }
 
+constexpr int kTblMax = 2048;  // block-table entries of a split staged in LDS
+
 // Element offset of token `t` of sequence `b`, KV head `hk` (or -1 when the
-// token's page is outside the cache).
+// token's page is outside the cache).  Paged: the page comes from the split's
+// block-table slice in LDS (tbl, first block blk_lo) when it was staged there,
+// else from the table in global memory.
 template <bool kPaged>
 __device__ inline long long kv_elem(const fa_gqa_decode_args& a, int b, int hk, int t,
-                                    long long s0, long long sh, long long st) {
+                                    long long s0, long long sh, long long st, const int* tbl,
+                                    int blk_lo, bool tbl_lds) {
   if constexpr (kPaged) {
     const int blk = t / a.block_size;
-    const int page = blk < a.max_blocks_per_seq
+    const int page = tbl_lds ? tbl[blk - blk_lo]
+                     : blk < a.max_blocks_per_seq
                          ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
                          : -1;
     if (page < 0 || page >= a.num_blocks) return -1;
@@ -143,6 +149,30 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   const unsigned char* kp = static_cast<const unsigned char*>(a.k);
   const unsigned char* vp = static_cast<const unsigned char*>(a.v);
 
+  // Paged: the split's block-table slice goes to LDS first.  A page lookup is then an
+  // LDS read; read from global memory it would be a vector load, and the wait for it
+  // (vmcnt counts in order) would also wait for the previous tile's K/V loads, leaving
+  // one tile in flight per wave.
+  __shared__ int tbl[kPaged ? kTblMax : 1];
+  int blk_lo = 0;
+  bool tbl_lds = false;
+  if constexpr (kPaged) {
+    if (ntok > 0) {
+      blk_lo = t0 / a.block_size;
+      const int nblk = (t1 - 1) / a.block_size - blk_lo + 1;
+      tbl_lds = nblk <= kTblMax;
+      if (tbl_lds) {
+        for (int i = threadIdx.x; i < nblk; i += kGThreads) {
+          const int blk = blk_lo + i;
+          tbl[i] = blk < a.max_blocks_per_seq
+                       ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
+                       : -1;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
   // Q^T operand: row c16, dims 32kk + 8G..+7 (zeros past D or past the last row)
   T8 qf[kKSteps];
 #pragma unroll
@@ -171,7 +201,8 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
       const int r = c * kTokPerCopy + lane / C;
       const int slot = lane % C;
       const int t = min(tile_start + r, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t);
+      const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t,
+                                          tbl, blk_lo, tbl_lds);
       const unsigned char* src =
           e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
@@ -182,7 +213,8 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int t = min(tile_start + 16 * h + c16, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t);
+      const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t,
+                                          tbl, blk_lo, tbl_lds);
       km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
