@@ -580,8 +580,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
-    // ---- prologue: tiles 0 and 1 requested (before Q, in the first pass) ----
-    auto prologue = [&]() {
+    // ---- prologue: tiles 0 and 1 requested (dense: before Q, in the first pass;
+    // sparse: Q is requested behind the rows of tiles 0 and 1, so that its
+    // latency overlaps the wait for those rows, which the tile copies need) ----
+    auto prologue = [&](bool with_q) {
       if constexpr (kMode == kDense) {
         prefetch_page(0);
         copy_all(dense_req(0, kv_buf0, &vq[0]));
@@ -590,7 +592,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         prefetch_page(2);
       } else {
         const RowPair r0l = load_row(0), r1l = load_row(1);
-        wait_vmem<0>();
+        if (with_q) {  // uniform
+          load_q();
+          wait_vmem<kQOps>();  // the rows (issued first) landed; Q may be in flight
+        } else {
+          wait_vmem<0>();
+        }
         const RowPair r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
         vq[0] = row_mask(r0);
         vq[1] = row_mask(r1);
@@ -609,8 +616,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         dequant_fp8_rowgroup(kv_buf0, wave);
       }
     };
-    prologue();
-    load_q();
+    prologue(true);
+    if constexpr (kMode == kDense) load_q();
     fp8_first_tile();
 
     float mref_start[2] = {ninf, ninf};
@@ -628,7 +635,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         for (int rt = 0; rt < kRowTiles; ++rt) acc[dt][rt] = floatx4{};
 
       if (pass > 0) {
-        prologue();
+        prologue(false);
         fp8_first_tile();
       }
 
