@@ -996,13 +996,14 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 // slot is unused (j >= topk, i < 0 or i >= cache_seqlens[b]).
 __global__ __launch_bounds__(256) void mla_sparse_rows_kernel(const fa_mla_decode_args a,
                                                               int32_t* __restrict__ rows,
-                                                              int topk_pad) {
-  const long long n = static_cast<long long>(a.batch) * a.s_q * topk_pad;
-  for (long long e = blockIdx.x * 256ll + threadIdx.x; e < n; e += 256ll * gridDim.x) {
-    const int j = static_cast<int>(e % topk_pad);
-    const long long bs = e / topk_pad;
-    const int s = static_cast<int>(bs % a.s_q);
-    const int b = static_cast<int>(bs / a.s_q);
+                                                              int topk_pad, int nrows) {
+  // grid: x over the row's slots, y over the (sequence, query token) rows -- no
+  // divisions per slot
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  for (int r = blockIdx.y; r < nrows; r += gridDim.y) {
+    const int b = r / a.s_q;
+    const int s = r - b * a.s_q;
+    if (j >= topk_pad) continue;
     int32_t out = -1;
     if (j < a.topk) {
       const int idx = a.indices[b * a.idx_stride_b + s * a.idx_stride_s + j];
@@ -1012,7 +1013,7 @@ __global__ __launch_bounds__(256) void mla_sparse_rows_kernel(const fa_mla_decod
         if (blk >= 0 && blk < a.num_kv_blocks) out = blk * kPage + (idx & 63);
       }
     }
-    rows[e] = out;
+    rows[static_cast<long long>(r) * topk_pad + j] = out;
   }
 }
 
@@ -1071,12 +1072,15 @@ extern "C" int fa_mla_sparse_rows(const fa_mla_decode_args* a, void* stream) {
   FA_CHECK_ARG(a->topk >= 1, "topk %d < 1", a->topk);
   FA_CHECK_ARG(a->num_kv_blocks >= 1, "num_kv_blocks %lld < 1",
                static_cast<long long>(a->num_kv_blocks));
+  FA_CHECK_ARG(a->topk <= (1 << 24), "topk %d too large", a->topk);
   const int topk_pad = fa::cdiv(a->topk, fa::kPage) * fa::kPage;
-  const long long n = static_cast<long long>(a->batch) * a->s_q * topk_pad;
-  const long long want = (n + 255) / 256;
-  const int grid = static_cast<int>(want < 4096 ? want : 4096);
-  hipLaunchKernelGGL(fa::mla_sparse_rows_kernel, dim3(grid), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), *a, a->sparse_rows, topk_pad);
+  const long long nrows = static_cast<long long>(a->batch) * a->s_q;
+  FA_CHECK_ARG(nrows < (1ll << 31), "batch * s_q too large");
+  const dim3 grid(static_cast<unsigned>(fa::cdiv(topk_pad, 256)),
+                  static_cast<unsigned>(nrows < 65535 ? nrows : 65535));
+  hipLaunchKernelGGL(fa::mla_sparse_rows_kernel, grid, dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *a, a->sparse_rows, topk_pad,
+                     static_cast<int>(nrows));
   FA_CHECK_HIP(hipGetLastError());
   return FA_OK;
 }
