@@ -119,7 +119,9 @@ __device__ inline void find_bin(TkSmem& sm, int cur, int need, bool descending, 
 // a position-ordered candidate list); slots v >= n hold key 0.
 
 // Radix select: thr = the topk-th largest key among slots [0, n), pos_end = one past
-// the last slot holding thr that is kept (ties keep the lowest slots).  n >= topk.
+// the last slot holding thr that is kept (ties keep the lowest slots).  n >= topk.  The
+// first pass's histogram (top 8 bits of every slot, sm.hist[0]) was filled while the
+// keys were loaded (hist0_add); a barrier must separate that from this call.
 template <int NQ>
 __device__ inline void radix_select(const unsigned int (&key)[4 * NQ], int n, int topk,
                                     TkSmem& sm, unsigned int& thr_out, int& pos_end_out) {
@@ -133,20 +135,18 @@ __device__ inline void radix_select(const unsigned int (&key)[4 * NQ], int n, in
   const int pad = NV * kTkThreads - n;
   unsigned int thr = 0;
   int need = topk, eq = 0, cur = 0;
-  zero_hist(sm.hist[0]);
-  __syncthreads();
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
     unsigned int* h = sm.hist[cur] + copy;
+    if (pass > 0) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const unsigned int k = key[j];
-      const bool in_group =
-          pass == 0 || static_cast<unsigned int>(static_cast<unsigned long long>(k) >> (shift + 8)) == thr;
-      if (in_group) atomicAdd(h + ((k >> shift) & 255u), 1u);
+      for (int j = 0; j < NV; ++j) {
+        const unsigned int k = key[j];
+        if ((k >> (shift + 8)) == thr) atomicAdd(h + ((k >> shift) & 255u), 1u);
+      }
+      __syncthreads();
     }
-    __syncthreads();
     find_bin(sm, cur, need, true, thr == 0u ? pad : 0);
     thr = (thr << 8) | static_cast<unsigned int>(sm.info[0]);
     need -= sm.info[1];
@@ -256,12 +256,23 @@ __device__ inline void ordered_emit(const unsigned int (&key)[4 * NQ], unsigned 
   }
 }
 
-// Keys of the n consecutive scores at src (n >= 1).  Every load is issued before any key
-// is formed (no wait between blocks).  Blocks of 4096 slots wholly below n use 16-byte
-// loads when src is 16-byte aligned; the block holding n reads element by element at
-// clamped (in-bounds) addresses; the blocks past it read nothing.  Uniform branches.
+// Clears the first histogram; call before the keys are loaded, then a barrier.
+__device__ inline void tk_begin(TkSmem& sm) { zero_hist(sm.hist[0]); }
+
+// The first radix pass's histogram entry of one key (top 8 bits), counted as the keys
+// arrive: the pass's atomics overlap the loads still in flight.
+__device__ inline void hist0_add(TkSmem& sm, unsigned int k) {
+  atomicAdd(sm.hist[0] + (threadIdx.x & (kTkCopies - 1)) * kTkCopyStride + (k >> 24), 1u);
+}
+
+// Keys of the n consecutive scores at src (n >= 1), counted into the first histogram as
+// they are formed.  Every load is issued before any key is formed; block q's keys wait
+// only for block q's loads.  Blocks of 4096 slots wholly below n use 16-byte loads when
+// src is 16-byte aligned; the block holding n reads element by element at clamped
+// (in-bounds) addresses; the blocks past it read nothing.  Uniform branches.
 template <int NQ>
-__device__ inline void load_score_keys(const float* src, int n, unsigned int (&key)[4 * NQ]) {
+__device__ inline void load_score_keys(const float* src, int n, unsigned int (&key)[4 * NQ],
+                                       TkSmem& sm) {
   const int tid = threadIdx.x;
   const int full = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? n / (4 * kTkThreads) : 0;
   floatx4 raw[NQ];
@@ -281,7 +292,10 @@ __device__ inline void load_score_keys(const float* src, int n, unsigned int (&k
   for (int q = 0; q < NQ; ++q) {
     const int p0 = 4 * (q * kTkThreads + tid);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) key[4 * q + c] = p0 + c < n ? order_key(raw[q][c]) : 0u;
+    for (int c = 0; c < 4; ++c) {
+      key[4 * q + c] = p0 + c < n ? order_key(raw[q][c]) : 0u;
+      hist0_add(sm, key[4 * q + c]);
+    }
   }
 }
 
@@ -325,8 +339,11 @@ __global__ __launch_bounds__(kTkThreads) void topk_indices_kernel(
     for (int i = tid; i < topk; i += kTkThreads) o[i] = i < n ? i : -1;
     return;
   }
+  tk_begin(sm);
+  __syncthreads();
   unsigned int key[4 * NQ];
-  load_score_keys<NQ>(scores + b * stride_b + t * stride_t, n, key);
+  load_score_keys<NQ>(scores + b * stride_b + t * stride_t, n, key, sm);
+  __syncthreads();
   unsigned int thr;
   int pos_end;
   radix_select<NQ>(key, n, topk, sm, thr, pos_end);
@@ -383,8 +400,11 @@ __global__ __launch_bounds__(kTkThreads) void topk_chunk_kernel(
     if (tid == 0) cand_cnt[blockIdx.x] = nc;
     return;
   }
+  tk_begin(sm);
+  __syncthreads();
   unsigned int key[4 * NQ];
-  load_score_keys<NQ>(src, nc, key);
+  load_score_keys<NQ>(src, nc, key, sm);
+  __syncthreads();
   unsigned int thr;
   int pos_end;
   radix_select<NQ>(key, nc, kl, sm, thr, pos_end);
@@ -444,6 +464,8 @@ __global__ __launch_bounds__(kTkThreads) void topk_merge_kernel(
     for (int i = 1; i < kTkMaxChunks; ++i) c += v >= pre[i] ? 1 : 0;
     return (lbase + c) * kl + (v - pre[c]);
   };
+  tk_begin(sm);
+  __syncthreads();
   unsigned int key[4 * NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
@@ -454,6 +476,9 @@ __global__ __launch_bounds__(kTkThreads) void topk_merge_kernel(
       key[4 * q + c] = v < n ? cand_key[where(v)] : 0u;
     }
   }
+#pragma unroll
+  for (int j = 0; j < 4 * NQ; ++j) hist0_add(sm, key[j]);
+  __syncthreads();
   unsigned int thr;
   int pos_end;
   radix_select<NQ>(key, n, topk, sm, thr, pos_end);
