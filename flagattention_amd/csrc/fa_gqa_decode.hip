@@ -81,9 +81,11 @@ constexpr int kTblMax = 2048;  // block-table entries of a split staged in LDS
 template <bool kPaged>
 __device__ inline long long kv_elem(const fa_gqa_decode_args& a, int b, int hk, int t,
                                     long long s0, long long sh, long long st, const int* tbl,
-                                    int blk_lo, bool tbl_lds) {
+                                    int blk_lo, bool tbl_lds, int bs_shift) {
   if constexpr (kPaged) {
-    const int blk = t / a.block_size;
+    // power-of-two block sizes (all the usual ones) shift instead of dividing: a
+    // division per load is tens of VALU instructions, ten times per tile and lane
+    const int blk = bs_shift >= 0 ? t >> bs_shift : t / a.block_size;
     const int page = tbl_lds ? tbl[blk - blk_lo]
                      : blk < a.max_blocks_per_seq
                          ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
@@ -156,6 +158,9 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   __shared__ int tbl[kPaged ? kTblMax : 1];
   int blk_lo = 0;
   bool tbl_lds = false;
+  const int bs_shift = kPaged && a.block_size > 0 && (a.block_size & (a.block_size - 1)) == 0
+                           ? __builtin_ctz(static_cast<unsigned int>(a.block_size))
+                           : -1;
   if constexpr (kPaged) {
     if (ntok > 0) {
       blk_lo = t0 / a.block_size;
@@ -190,11 +195,63 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   T8 kf[2][2][kKSteps];  // [buffer][token half][k-step]
   // keys of the tile whose page is inside the cache (bit j: token j of the tile)
   unsigned int kmask[2] = {0u, 0u};
+  // Paged, pages of 16 or more tokens (a power of two) and tiles starting on a
+  // multiple of 16: each 16-token half of a tile lies in one page, so a tile needs two
+  // page ids, wave-uniform.  They are fetched with scalar loads one tile ahead (the
+  // wave's next tile is u + 4), so no load address of a tile waits on a lookup.
+  const bool page_pairs = kPaged && bs_shift >= 4 && (t0 & 15) == 0;
+  const int32_t* const bt_row = kPaged ? a.block_table + static_cast<long long>(b) * a.bt_stride_b
+                                       : nullptr;
+  auto half_page = [&](int u, int h) -> int {  // page of tile u's half h, -1 if none
+    const int t = min(t0 + kGTile * u + 16 * h, t1 - 1);
+    const int blk = t >> bs_shift;
+    const int pg = blk < a.max_blocks_per_seq ? sload(bt_row + blk) : -1;
+    return pg >= 0 && pg < a.num_blocks ? pg : -1;
+  };
+  int pg_next0 = -1, pg_next1 = -1;  // pages of the next tile this wave issues
   auto issue = [&](int u, auto bt) {
     constexpr int buf = decltype(bt)::value;
     unsigned char* const vb = (buf == 0 ? vbuf0 : vbuf1) + wave * kTileB;
     const int tile_start = t0 + kGTile * u;
     const int last = t1 - 1;
+    if (page_pairs) {  // uniform
+      const int p0 = pg_next0, p1 = pg_next1;
+      if (u + 4 < ntiles) {
+        pg_next0 = half_page(u + 4, 0);
+        pg_next1 = half_page(u + 4, 1);
+      }
+      const int bmask = (1 << bs_shift) - 1;
+      auto elem = [&](int r, int t, long long s0, long long sh, long long st) -> long long {
+        const int pg = r < 16 ? p0 : p1;
+        return pg < 0 ? -1ll : pg * s0 + hk * sh + (t & bmask) * st;
+      };
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c) {
+        const int r = c * kTokPerCopy + lane / C;
+        const int slot = lane % C;
+        const int t = min(tile_start + r, last);
+        const long long e = elem(r, t, a.v_stride_0, a.v_stride_h, a.v_stride_t);
+        const unsigned char* src =
+            e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (FA_LDS void*)(vb + c * 1024), 16, 0, 0);
+      }
+      unsigned int km = 0u;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int t = min(tile_start + 16 * h + c16, last);
+        const long long e = elem(16 * h, t, a.k_stride_0, a.k_stride_h, a.k_stride_t);
+        km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
+#pragma unroll
+        for (int kk = 0; kk < kKSteps; ++kk) {
+          const int d0 = 32 * kk + 8 * G;
+          const unsigned char* src = (e >= 0 && d0 < D) ? kp + 2 * (e + d0) : g_gqa_zero;
+          kf[buf][h][kk] = *reinterpret_cast<const T8*>(src);
+        }
+      }
+      kmask[buf] = km;
+      return;
+    }
     // V: copy c, lane -> token c * kTokPerCopy + lane / C, slot lane % C
 #pragma unroll
     for (int c = 0; c < kCopies; ++c) {
@@ -202,7 +259,7 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
       const int slot = lane % C;
       const int t = min(tile_start + r, last);
       const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t,
-                                          tbl, blk_lo, tbl_lds);
+                                          tbl, blk_lo, tbl_lds, bs_shift);
       const unsigned char* src =
           e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
@@ -214,7 +271,7 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
     for (int h = 0; h < 2; ++h) {
       const int t = min(tile_start + 16 * h + c16, last);
       const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t,
-                                          tbl, blk_lo, tbl_lds);
+                                          tbl, blk_lo, tbl_lds, bs_shift);
       km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
@@ -297,6 +354,10 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   };
 
   if (wave < ntiles) {
+    if (page_pairs) {
+      pg_next0 = half_page(wave, 0);
+      pg_next1 = half_page(wave, 1);
+    }
     issue(wave, IntTag<0>{});
     int u = wave;
     for (;;) {
