@@ -156,3 +156,24 @@ def test_indices_drive_sparse_decode():
     torch.cuda.synchronize()
     assert (o1.cpu().float() - ref_out).abs().max() < 2e-2
     assert (l1.cpu() - ref_lse).abs().max() < 1e-3
+
+
+def test_c_abi_without_workspace_matches_two_stage():
+    """fa_mla_topk_indices with no workspace runs the single-stage path; a long row gives
+    the same indices as the two-stage path the Python operator takes."""
+    need_gpu()
+    from flagattention_amd import _lib
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(21)
+    scores = torch.randn((3, 1, 65536), generator=gen).to(DEV)
+    lens = torch.tensor([65536, 40000, 20000], dtype=torch.int32, device=DEV)
+    assert lib.fa_mla_topk_workspace_bytes(3, 1, 65536, 2048) > 0
+    two = flag_attn.topk_indices(scores, lens, 2048)
+    one = torch.empty_like(two)
+    _lib.check(lib.fa_mla_topk_indices(scores.data_ptr(), 65536, 65536, lens.data_ptr(), 3, 1,
+                                       65536, 2048, 0, one.data_ptr(), None, 0,
+                                       torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(one.cpu(), two.cpu())
+    want = tko.topk_indices_ref(scores.cpu().numpy(), [65536, 40000, 20000], 2048, False)
+    assert np.array_equal(one.cpu().numpy(), want)
