@@ -541,7 +541,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       const unsigned char* p =
           kv + static_cast<unsigned long long>(rr >> 6) * static_cast<unsigned int>(block_stride) +
           __umul24(rr & 63u, static_cast<unsigned int>(row_stride));
-      return r >= 0 ? p : zero_row;
+      const unsigned char* q = r >= 0 ? p : zero_row;
+      asm volatile("" : "+v"(q));  // the select stays here (see gather_req)
+      return q;
     };
     // sparse: key mask of a tile from its rows (lanes 0..31 hold rows 0..31)
     auto row_mask = [&](RowPair r) -> unsigned int {
@@ -555,6 +557,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
                                                0x00020000);  // unused
       c.src = row_ptr(r.g);
       if constexpr (kMode == kSparseBf16) c.src += 16 * ((lane & 7) ^ lrow);
+      // one opaque pointer per tile (and the select kept in row_ptr):
+      // otherwise the compiler distributes the row_ptr select over the lane
+      // and block offsets, keeps the masked-row pointers live across the
+      // loop, spills them, and each reload then waits for every load in
+      // flight (vmcnt counts in order), the next tile's copies included
+      asm volatile("" : "+v"(c.src));
       c.voff = 0;
       c.dst = buf + wave * kRowGroupBytes;
       return c;
@@ -747,14 +755,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         // softmax(t) of the owned rows: row 32*wave + 16rt + i16, tokens
         // 16tt + 4G + i (8 per row and lane)
         const bool partial = vm != ~0u || t >= causal_from;  // uniform
-        // dense, full tile, both references set (uniform; the usual case):
-        // scores relative to the reference in one fma each, the running max
-        // kept absolute (the reference plus the relative max), and both row
-        // tiles in one branch-free block so that their dependency chains
-        // interleave (1% faster than one row tile after the other).  Sparse
-        // tiles are partial about half the time, where the test costs more
-        // than it saves.
-        const bool fast = kMode == kDense && !partial &&
+        // full tile, both references set (uniform; the usual case): scores
+        // relative to the reference in one fma each, the running max kept
+        // absolute (the reference plus the relative max), and both row tiles
+        // in one branch-free block so that their dependency chains interleave
+        // (1% faster than one row tile after the other for dense decode, 1-2%
+        // for sparse decode although about half of its tiles are partial).
+        const bool fast = !partial &&
                           __ballot(mref[0] == ninf || mref[1] == ninf) == 0ull;
         if (fast) {
           float sv[2][8];
