@@ -285,15 +285,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     }
   };
 
-  // query token of the rows this lane computes S and P for (32*wave + 16rt
-  // + i16), for the causal limit
-  int own_s[2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    int hh;
-    map_row(32 * wave + 16 * rt + i16, own_s[rt], hh);
-  }
-
   const float scale_log2 = a.softmax_scale * kLog2e;
   const float ninf = -__builtin_inff();
   const int topk_pad = (a.topk + kPage - 1) / kPage * kPage;
@@ -386,6 +377,21 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     const int ns0 = sload(a.num_splits + b);
     const int nsplit = sload(a.num_splits + b + 1) - ns0;
     const bool split_ok = ns0 >= 0 && split_local >= 0 && ns0 + split_local < max_split;
+    // query token of the rows this lane computes S and P for (32*wave +
+    // 16rt + i16), for the causal limit: rebuilt per segment from a fresh
+    // lane id (kept from the kernel start it is spilled, and its reload,
+    // behind the segment's first loads, waits for all of them)
+    int own_s[2] = {0, 0};
+    if constexpr (kMode == kDense) {
+      if (a.causal) {
+        const int ln = fresh_lane();
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          int hh;
+          map_row(32 * wave + 16 * rt + (ln & 15), own_s[rt], hh);
+        }
+      }
+    }
     // Keys owned row rt may see (dense, bottom-right causal), relative to
     // the segment start; tiles from causal_from on need the per-row check.
     auto row_limit = [&](int rt) -> int {
@@ -907,7 +913,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       l_own[rt] = sum_xor32(sum_xor16(lsum[rt]));
-      if (G == 0) reinterpret_cast<float*>(sm.p)[32 * wave + 16 * rt + i16] = l_own[rt];
+      const int ln = fresh_lane();  // the slot rebuilt here, not kept (spilled) from the start
+      if (ln < 16) reinterpret_cast<float*>(sm.p)[32 * wave + 16 * rt + ln] = l_own[rt];
     }
     barrier();
     const long long pbase = static_cast<long long>(ns0 + split_local) * rows_total;
