@@ -70,7 +70,7 @@ constexpr int kDimTiles = kDv / 4 / 16;          // 8 16-dim tiles of O^T per wa
 constexpr int kRowTiles = kRows / 16;            // 8 16-row tiles
 constexpr int kCopiesPerWave = kChunkGroups;     // 9 wave-wide copies per tile
 constexpr int kQOps = 2 * kQkSteps;              // 36 Q^T operands (k-step, row tile) per wave
-constexpr int kQLds = 11;                         // sparse: the first ones live in LDS, not VGPRs
+constexpr int kQLds = 4;                          // sparse: the first ones live in LDS, not VGPRs
 
 enum Mode { kDense = 0, kSparseBf16 = 1, kSparseFp8 = 2 };
 
@@ -408,7 +408,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // Dense decode keeps all 36 operands in VGPRs (its loop needs about 225
     // of the 256; no LDS reads for Q, 3.5% faster than 11 in LDS).  The sparse
     // loops need more registers (row ids, gathers): there the first kQLds
-    // operands sit in this wave's LDS slot, read at the start of each QK with
+    // operands (4: the fewest that leave the loops unspilled; each one in
+    // VGPRs instead saves QK a 1 KB LDS read per tile, measured 2-3% from 11
+    // to 4) sit in this wave's LDS slot, read at the start of each QK with
     // the first K operands, and go there directly (LDS-destination loads, 16
     // bytes per lane = the slot's lane layout).  The AGPRs hold the O
     // accumulators.  Issued behind the first two tile requests, so that a
@@ -449,14 +451,23 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // converted in place one tile ahead by the wave that loaded each
     // row-group).  Every lane issues the same loads for every tile (masked
     // rows / pages read zeros), so the vmcnt waits are constants.
-    // dense: page of the next tile to request, looked up one step ahead
-    int next_page = -1;
-    auto prefetch_page = [&](int u) {
-      if ((u & 1) == 0) {
-        const int blk = blk_lo + (u >> 1);
-        next_page = (u < ntiles && blk < a.max_blocks_per_seq) ? sload(bt + blk) : -1;
-      }
+    // dense: page ids by vector loads, issued a step before their use and
+    // ahead of that step's tile copies, so that the copy wait covers them.
+    // (A scalar load would be waited for by the next LDS wait of the step:
+    // scalar loads return out of order and share the LDS counter.)  The
+    // block index is clamped into the row (max_blocks_per_seq >= 1, checked
+    // on the host); page_of applies the bounds.
+    auto load_page = [&](int u) -> int {
+      int blk = min(blk_lo + (u >> 1), a.max_blocks_per_seq - 1);
+      asm volatile("" : "+v"(blk));
+      return bt[blk];
     };
+    auto page_of = [&](int u, int loaded) -> int {  // uniform; -1: no page
+      const int blk = blk_lo + (u >> 1);
+      const int p = __builtin_amdgcn_readfirstlane(loaded);
+      return (u < ntiles && blk < a.max_blocks_per_seq) ? p : -1;
+    };
+    int page_q = -1;  // dense: page of tile t+2 as loaded during step t-1
     // dense: buffer resource of tile u's half page (rows past the sequence,
     // or a page id outside the cache, read as zeros) and its key mask
     // A tile request: this wave's nine 1 KB blocks of the tile, issued one
@@ -506,13 +517,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     };
     // dense: request of tile u's half page (rows past the sequence, or a page
     // id outside the cache, read as zeros); *mask = its key mask
-    auto dense_req = [&](int u, unsigned char* buf, unsigned int* mask) -> CopyReq {
+    auto dense_req = [&](int u, int page, unsigned char* buf, unsigned int* mask) -> CopyReq {
       const int blk = blk_lo + (u >> 1), half = u & 1;
-      const bool ok = u < ntiles && next_page >= 0 && next_page < a.num_kv_blocks;
+      const bool ok = u < ntiles && page >= 0 && page < a.num_kv_blocks;
       const int start = blk * kPage + kTileRows * half;
       const int nrows = ok ? max(0, min(seqlen - start, kTileRows)) : 0;
       const unsigned char* base =
-          kv + (ok ? next_page : 0) * block_stride + kTileRows * half * row_stride;
+          kv + (ok ? page : 0) * block_stride + kTileRows * half * row_stride;
       CopyReq c;
       c.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(uniform(base)), 0,
                                                uniform(nrows * static_cast<int>(row_stride)),
@@ -599,11 +610,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // latency overlaps the wait for those rows, which the tile copies need) ----
     auto prologue = [&](bool with_q) {
       if constexpr (kMode == kDense) {
-        prefetch_page(0);
-        copy_all(dense_req(0, kv_buf0, &vq[0]));
-        prefetch_page(1);
-        copy_all(dense_req(1, kv_buf1, &vq[1]));
-        prefetch_page(2);
+        const int p0 = load_page(0);  // tiles 0 and 1 share a page
+        copy_all(dense_req(0, page_of(0, p0), kv_buf0, &vq[0]));
+        copy_all(dense_req(1, page_of(1, p0), kv_buf1, &vq[1]));
+        page_q = load_page(2);
       } else {
         const RowPair r0l = load_row(0), r1l = load_row(1);
         if (with_q) {  // uniform
@@ -675,7 +685,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         CopyReq creq;  // tile t+2, issued block by block during QK(t) or PV(t)
         if constexpr (kMode == kDense) {
           unsigned int m;
-          creq = dense_req(t + 2, b_cp, &m);
+          creq = dense_req(t + 2, page_of(t + 2, page_q), b_cp, &m);
+          page_q = load_page(t + 3);  // ahead of tile t+2's copies
           vq[0] = vq[1];
           vq[1] = m;
         } else if constexpr (kMode == kSparseBf16) {
@@ -870,7 +881,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
             __builtin_amdgcn_sched_barrier(0);
           });
         }
-        if constexpr (kMode == kDense) prefetch_page(t + 3);  // lands by the next barrier
       };
       // Whole rounds of three steps, then the remainder (the loop back-edge
       // is only taken after step 2, which keeps the compiler's view of the
@@ -1074,6 +1084,8 @@ extern "C" int fa_mla_decode_dense(const fa_mla_decode_args* a, void* stream) {
   if (rc != FA_OK) return rc;
   FA_CHECK_ARG(a->kv_row_stride >= 2 * fa::kDqk, "kv_row_stride %lld < 1152",
                static_cast<long long>(a->kv_row_stride));
+  FA_CHECK_ARG(a->max_blocks_per_seq >= 1, "block_table has %d columns (needs >= 1)",
+               a->max_blocks_per_seq);
   return fa::launch_decode<fa::kDense>(a, static_cast<hipStream_t>(stream));
 }
 

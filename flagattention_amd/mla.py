@@ -208,6 +208,7 @@ def _check_decode_args(q, k_cache, block_table, cache_seqlens, head_dim_v, tile_
     _require(block_table.dtype == torch.int32 and block_table.dim() == 2,
              "block_table must be int32 [batch, max_blocks]")
     _require(block_table.shape[0] == batch, "block_table batch mismatch")
+    _require(block_table.shape[1] >= 1, "block_table needs at least one column")
     _require(block_table.stride(1) == 1, "block_table rows must be contiguous")
     _require(cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (batch,)
              and cache_seqlens.is_contiguous(), "cache_seqlens must be contiguous int32 [batch]")

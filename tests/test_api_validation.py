@@ -38,6 +38,7 @@ def test_error_type_is_value_and_assertion_error():
     (lambda a: a.update(k_cache=torch.zeros((4, 32, 1, 576), dtype=torch.bfloat16)), "block size"),
     (lambda a: a.update(k_cache=torch.zeros((4, 64, 2, 576), dtype=torch.bfloat16)), "KV head"),
     (lambda a: a.update(block_table=a["block_table"].long()), "block_table"),
+    (lambda a: a.update(block_table=a["block_table"][:, :0]), "at least one column"),
     (lambda a: a.update(cache_seqlens=a["cache_seqlens"].long()), "cache_seqlens"),
     (lambda a: a.update(num_splits=torch.zeros((2,), dtype=torch.int32)), "num_splits"),
     (lambda a: a.update(tile_scheduler_metadata=torch.zeros((8, 4), dtype=torch.int32)),
