@@ -85,6 +85,9 @@ struct __attribute__((aligned(16))) Smem {
   unsigned char p[kRows * 64];
   // Q^T operands that do not fit in VGPRs: [wave][operand][lane]
   bf16x8 qx[4][kQLds][64];
+  // sparse: each wave's ring of tile row lists, tile u in slot u % 3 (lanes
+  // 32..63 repeat rows 0..31)
+  int32_t rows[4][3][64];
 };
 
 // Source of masked gather rows: every lane issues its copy (so each wave has
@@ -436,8 +439,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           if (j >= kQInLds) {
             qf[j - kQInLds] = *reinterpret_cast<const bf16x8*>(qrow + 32 * kq);
           } else {
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(qrow + 32 * kq),
-                                             (FA_LDS void*)(&sm.qx[wave][j][0]), 16, 0, 0);
+            lds_dma16(qrow + 32 * kq, (FA_LDS void*)(&sm.qx[wave][j][0]));
           }
         }
       }
@@ -484,8 +486,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       if constexpr (kMode == kDense) {
         copy_block_buf<Gc>(c.rs, c.dst, c.voff);
       } else if constexpr (kMode == kSparseBf16) {
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(c.src + 128 * Gc),
-                                         (FA_LDS void*)(c.dst + Gc * kBlockBytes), 16, 0, 0);
+        lds_dma16(c.src + 128 * Gc, (FA_LDS void*)(c.dst + Gc * kBlockBytes));
       } else {
         // fp8 raw layout (c.src = this lane's row): codes 128Gc + 16(lane%8)
         // for Gc < 4, the scales, then the rope chunk of the bf16 slot
@@ -502,8 +503,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           src = c.src + 528 + 16 * (l8 ^ lrow);
           dst = c.dst + 8 * kBlockBytes;
         }
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (FA_LDS void*)dst,
-                                         16, 0, 0);
+        lds_dma16(src, (FA_LDS void*)dst);
       }
     };
     constexpr int kCopies = kMode == kSparseFp8 ? kFp8Copies : kCopiesPerWave;
@@ -534,19 +534,27 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       *mask = nrows >= kTileRows ? ~0u : ((1u << nrows) - 1u);
       return c;
     };
-    // sparse: physical rows of tile u, as loaded, twice: m = tile row
-    // (lane % 32), the key-mask layout; g = tile row 8*wave + lane/8, the row
-    // this lane copies (two loads instead of a lane exchange that would wait
-    // on the LDS queue).  The tile index is clamped so the loads stay inside
-    // the row list; row_valid masks tiles past the end (-1: masked).  The
-    // select waits for the loads, so it is applied only where the rows are used.
+    // sparse: physical rows of tile u.  request_rows copies the tile's row
+    // list into this wave's LDS ring (one LDS-destination load, counted in
+    // vmcnt with the tile copies; loading the rows into VGPRs instead would
+    // have the compiler wait for them behind the copies, which it does not
+    // see); read_rows then takes them twice: m = tile row (lane % 32), the
+    // key-mask layout; g = tile row 8*wave + lane/8, the row this lane
+    // copies.  The tile index is clamped so the loads stay inside the row
+    // list; row_valid masks tiles past the end (-1: masked).
     struct RowPair {
       int32_t m, g;
     };
-    auto load_row = [&](int u) -> RowPair {
+    auto request_rows = [&](int u) {
       const int uu = u < ntiles ? u : ntiles - 1;
-      const int32_t* base = srows + tok_lo + kTileRows * uu;
-      return RowPair{base[lane & 31], base[8 * wave + lrow]};
+      const int ln = fresh_lane();  // rebuilt here: kept, the lane term is spilled
+      lds_dma4(srows + tok_lo + kTileRows * uu + (ln & 31),
+               (FA_LDS void*)(&sm.rows[wave][u % 3][0]));
+    };
+    auto read_rows = [&](int u) -> RowPair {  // after a wait that covers request_rows(u)
+      __builtin_amdgcn_sched_barrier(0);
+      const int32_t* ring = sm.rows[wave][u % 3];
+      return RowPair{ring[lane & 31], ring[8 * wave + lrow]};
     };
     auto row_valid = [&](int u, RowPair r) -> RowPair {
       return u < ntiles ? r : RowPair{-1, -1};
@@ -584,7 +592,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       c.dst = buf + wave * kRowGroupBytes;
       return c;
     };
-    RowPair rq0{-1, -1}, rq1{-1, -1};  // sparse: rows of tiles t+2 and t+3
     // key masks of tiles t, t+1 (scalar queue; bit j: token j of the tile)
     unsigned int vq[2] = {0u, 0u};
 
@@ -606,7 +613,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     };
 
     // ---- prologue: tiles 0 and 1 requested (dense: before Q, in the first pass;
-    // sparse: Q is requested behind the rows of tiles 0 and 1, so that its
+    // sparse: Q is requested beside the rows of tiles 0 and 1, so that its
     // latency overlaps the wait for those rows, which the tile copies need) ----
     auto prologue = [&](bool with_q) {
       if constexpr (kMode == kDense) {
@@ -615,22 +622,23 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         copy_all(dense_req(1, page_of(1, p0), kv_buf1, &vq[1]));
         page_q = load_page(2);
       } else {
-        const RowPair r0l = load_row(0), r1l = load_row(1);
-        if (with_q) {  // uniform
-          load_q();
-          wait_vmem<kQOps>();  // the rows (issued first) landed; Q may be in flight
-        } else {
-          wait_vmem<0>();
-        }
-        const RowPair r0 = row_valid(0, r0l), r1 = row_valid(1, r1l);
+        request_rows(0);
+        request_rows(1);
+        // Q is requested beside the rows of tiles 0 and 1, and both are
+        // waited for before the first copies: the compiler then knows Q has
+        // landed (it does not see the row and tile loads, so a wait for part
+        // of Q would come out as a full wait inside the loop)
+        if (with_q) load_q();  // uniform
+        wait_vmem<0>();
+        const RowPair r0 = row_valid(0, read_rows(0)), r1 = row_valid(1, read_rows(1));
         vq[0] = row_mask(r0);
         vq[1] = row_mask(r1);
         // issue order copies(0), rows(2), copies(1), rows(3): the order the
         // steps keep (rows two tiles before their copies)
         copy_all(gather_req(r0, kv_buf0));
-        rq0 = load_row(2);
+        request_rows(2);
         copy_all(gather_req(r1, kv_buf1));
-        rq1 = load_row(3);
+        request_rows(3);
       }
     };
     // fp8: tile 0 is converted once its raw copies landed (tile t+1 by step t)
@@ -674,7 +682,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         if constexpr (kMode == kSparseFp8) {
           wait_vmem<0>();
         } else if constexpr (kMode == kSparseBf16) {
-          wait_vmem<kCopiesPerWave + 2>();  // also the rows of tile t+2 (two loads)
+          wait_vmem<kCopiesPerWave + 1>();  // also the rows of tile t+2 (one load)
         } else {
           wait_vmem<kCopiesPerWave>();
         }
@@ -690,9 +698,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           vq[0] = vq[1];
           vq[1] = m;
         } else if constexpr (kMode == kSparseBf16) {
-          const RowPair r = row_valid(t + 2, rq0);
-          rq0 = rq1;
-          rq1 = load_row(t + 4);  // before the copies: a later wait covers it
+          const RowPair r = row_valid(t + 2, read_rows(t + 2));
+          request_rows(t + 4);  // before the copies: a later wait covers it
           creq = gather_req(r, b_cp);
           vq[0] = vq[1];
           vq[1] = row_mask(r);
@@ -701,10 +708,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           // with the wait above) becomes bf16; it is read from step t+1 on.
           // (Converting it at the end of this step instead, which gives its
           // copies half a step more, measured 1.7% slower.)
+          // (The rows of tile t+2 are read first: their LDS latency then
+          // passes under the conversion.)
+          const RowPair rr = read_rows(t + 2);
           dequant_fp8_rowgroup(FA_KVBUF((K + 1) % 3), wave);
-          const RowPair r = row_valid(t + 2, rq0);
-          rq0 = rq1;
-          rq1 = load_row(t + 4);
+          const RowPair r = row_valid(t + 2, rr);
+          request_rows(t + 4);
           creq = gather_req(r, b_cp);
           vq[0] = vq[1];
           vq[1] = row_mask(r);
@@ -855,13 +864,20 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(sv[2 * j], sv[2 * j + 1]);
           *reinterpret_cast<uintx4*>(sm.p + lo.p + (2 * wave + rt) * 1024) = w;
         }
-        barrier();
+        // The V^T operands not read before the softmax are requested before
+        // the barrier, which then waits only for the P writes ahead of them
+        // (the loop issues no scalar loads), so their latency overlaps it.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dt = kVPre; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lds_upto<2 * (kDimTiles - kVPre)>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
 
         // PV(t): dims 128*wave.. of all 128 rows, 64 MFMAs; P^T read two row
         // tiles ahead
         {
-#pragma unroll
-          for (int dt = kVPre; dt < kDimTiles; ++dt) va[dt] = v_read(lo, b_cur, dt);
           bf16x8 pb[2];
           auto p_read = [&](int rt) -> bf16x8 {
             return *reinterpret_cast<const bf16x8*>(sm.p + lo.p + rt * 1024);

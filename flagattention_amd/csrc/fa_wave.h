@@ -17,6 +17,13 @@ __device__ inline T sload(const T* p) {
 }
 
 __device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
+// s_waitcnt lgkmcnt(N): all but the last N LDS operations done (LDS operations
+// complete in order; only valid while no scalar load is outstanding)
+template <int N>
+__device__ inline void wait_lds_upto() {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt is four bits");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
 // Work-group barrier that also fences the instruction scheduler: the phases
 // between barriers are laid out by hand, so nothing may move across.
 __device__ inline void barrier() {
@@ -42,6 +49,35 @@ __device__ inline int fresh_lane() {
   int l;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
   return l;
+}
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at lds + 16 l.  Issued from
+// inline asm rather than the builtin: the compiler books the builtin as a flat
+// access that may still be pending on the LDS counter, after which it can
+// only wait for an LDS read with lgkmcnt(0), i.e. behind every LDS read in
+// flight, which defeats reading operands ahead.  The hardware counts these
+// loads in vmcnt alone; the kernels wait for them with explicit vmcnt counts,
+// and the compiler's own vmcnt waits, not knowing of them, can only come out
+// stricter.  (m0 holds the LDS address; one wait state after writing it.)
+__device__ inline void lds_dma16(const void* src, FA_LDS void* lds) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<__SIZE_TYPE__>(lds)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(m0)
+               : "memory", "m0");
+}
+
+// The same for 4 bytes per lane (global_load_lds_dword): lane l's word lands
+// at lds + 4 l.
+__device__ inline void lds_dma4(const void* src, FA_LDS void* lds) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<__SIZE_TYPE__>(lds)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(src), "s"(m0)
+               : "memory", "m0");
 }
 
 // LDS transpose read (ds_read_b64_tr_b16).  Within each 16-lane group, result
