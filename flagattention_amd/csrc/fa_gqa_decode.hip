@@ -233,8 +233,7 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
         const long long e = elem(r, t, a.v_stride_0, a.v_stride_h, a.v_stride_t);
         const unsigned char* src =
             e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                         (FA_LDS void*)(vb + c * 1024), 16, 0, 0);
+        lds_dma16(src, (FA_LDS void*)(vb + c * 1024));
       }
       unsigned int km = 0u;
 #pragma unroll
@@ -262,8 +261,7 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
                                           tbl, blk_lo, tbl_lds, bs_shift);
       const unsigned char* src =
           e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                       (FA_LDS void*)(vb + c * 1024), 16, 0, 0);
+      lds_dma16(src, (FA_LDS void*)(vb + c * 1024));
     }
     // K: token half h, lane -> token 16h + lane % 16, dims 32kk + 8G..+7
     unsigned int km = 0u;
