@@ -187,9 +187,20 @@ __device__ inline unsigned int pack_bf16x2(float a, float b) {
 constexpr int kFp8Copies = 6;          // wave-wide 16-byte copies per row-group
 constexpr int kFp8ScaleOff = 4096;
 
-__device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
-  // addresses rebuilt from a fresh lane id: kept live across the loop they
-  // would be spilled, and each reload would stall the conversion
+// The conversion in two parts, so that a step can spread it over its MFMAs:
+// fp8_load reads this lane's 64 codes and their scale (all the row-group's
+// reads, before any write), fp8_store<I, H> converts and writes one 16-byte
+// bf16 chunk of them (8 calls cover the lane).  Addresses are rebuilt from a
+// fresh lane id: kept live across the loop they would be spilled, and each
+// reload would stall the conversion.
+struct Fp8Codes {
+  uintx4 code[4];
+  float scale;
+  int base;  // byte offset of the lane's row r, chunk-group e in the row-group
+  int r;     // row of the lane in the row-group (the chunk swizzle)
+  int eh;    // e / 2: the lane's rotation of its four pieces
+};
+__device__ inline Fp8Codes fp8_load(const unsigned char* buf, int wave) {
   const int lane = fresh_lane();
   const int r = lane >> 3, e = lane & 7;  // row r of the group, codes 64e..64e+63
   const unsigned char* rg = buf + wave * kRowGroupBytes;
@@ -198,27 +209,42 @@ __device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
   // reads of one instruction then fall in 16 different bank groups per 16 lanes, and
   // its writes in 8 (2-way) instead of 2 (8-way).
   const int rot = e >> 1;
-  uintx4 code[4];
+  Fp8Codes c;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    code[i] = *reinterpret_cast<const uintx4*>(src + 16 * ((i + rot) & 3));
-  const float scale = *reinterpret_cast<const float*>(rg + kFp8ScaleOff + 128 * r + 4 * (e >> 1));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = (i + rot) & 3;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // 8 codes -> 8 bf16 = one 16-byte chunk
-      const unsigned int w0 = code[i][2 * h], w1 = code[i][2 * h + 1];
-      floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
-      floatx2 c = fp8x2_to_f32<false>(w1), d = fp8x2_to_f32<true>(w1);
-      uintx4 o;
-      o[0] = pack_bf16x2(a[0] * scale, a[1] * scale);
-      o[1] = pack_bf16x2(b[0] * scale, b[1] * scale);
-      o[2] = pack_bf16x2(c[0] * scale, c[1] * scale);
-      o[3] = pack_bf16x2(d[0] * scale, d[1] * scale);
-      *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * m + h)) = o;
-    }
-  }
+    c.code[i] = *reinterpret_cast<const uintx4*>(src + 16 * ((i + rot) & 3));
+  c.scale = *reinterpret_cast<const float*>(rg + kFp8ScaleOff + 128 * r + 4 * (e >> 1));
+  c.base = (kChunkGroups * wave + e) * kBlockBytes + 128 * r;  // tile_off(8 wave + r, 8 e)
+  c.r = r;
+  c.eh = rot;
+  return c;
+}
+// Byte offset of piece I, half H of the lane: tile_off(8 wave + r, 8 e + 2 m + H).
+template <int I, int H>
+__device__ inline int fp8_store_off(const Fp8Codes& c) {
+  return c.base + 16 * ((2 * ((I + c.eh) & 3) + H) ^ c.r);
+}
+template <int I, int H>  // piece I of the four, half H: 8 codes -> one 16-byte bf16 chunk
+__device__ inline void fp8_store(unsigned char* buf, int wave, const Fp8Codes& c) {
+  const int lane = fresh_lane();
+  const int r = lane >> 3, e = lane & 7;
+  const int m = (I + (e >> 1)) & 3;
+  const unsigned int w0 = c.code[I][2 * H], w1 = c.code[I][2 * H + 1];
+  floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
+  floatx2 d = fp8x2_to_f32<false>(w1), f = fp8x2_to_f32<true>(w1);
+  uintx4 o;
+  o[0] = pack_bf16x2(a[0] * c.scale, a[1] * c.scale);
+  o[1] = pack_bf16x2(b[0] * c.scale, b[1] * c.scale);
+  o[2] = pack_bf16x2(d[0] * c.scale, d[1] * c.scale);
+  o[3] = pack_bf16x2(f[0] * c.scale, f[1] * c.scale);
+  *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * m + H)) = o;
+}
+__device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
+  const Fp8Codes c = fp8_load(buf, wave);
+  static_for<8>([&](auto pt) {
+    constexpr int P = decltype(pt)::value;
+    fp8_store<P / 2, P % 2>(buf, wave, c);
+  });
 }
 
 template <int kMode>
@@ -676,14 +702,14 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         constexpr int K = decltype(tag)::value;  // t % 3
         unsigned char* const b_cur = FA_KVBUF(K);
         unsigned char* const b_cp = FA_KVBUF((K + 2) % 3);
-        // this wave's copies of tile t landed (those of t+1 may be in flight;
-        // fp8: those of t+1 too, converted below), then everyone's; everyone
-        // is done with step t-1, which frees buffer (t+2) % 3
-        if constexpr (kMode == kSparseFp8) {
-          wait_vmem<0>();
-        } else if constexpr (kMode == kSparseBf16) {
+        // this wave's copies of tile t landed (those of t+1 may be in flight),
+        // then everyone's; everyone is done with step t-1, which frees buffer
+        // (t+2) % 3.  fp8: tile t was converted during PV(t-1) by the waves
+        // that loaded it, after a wait that also covered the rows of tile t+2,
+        // so only the barrier is needed.
+        if constexpr (kMode == kSparseBf16) {
           wait_vmem<kCopiesPerWave + 1>();  // also the rows of tile t+2 (one load)
-        } else {
+        } else if constexpr (kMode == kDense) {
           wait_vmem<kCopiesPerWave>();
         }
         barrier();
@@ -704,15 +730,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           vq[0] = vq[1];
           vq[1] = row_mask(r);
         } else {
-          // fp8: this wave's row-group of tile t+1 (its raw copies landed
-          // with the wait above) becomes bf16; it is read from step t+1 on.
-          // (Converting it at the end of this step instead, which gives its
-          // copies half a step more, measured 1.7% slower.)
-          // (The rows of tile t+2 are read first: their LDS latency then
-          // passes under the conversion.)
-          const RowPair rr = read_rows(t + 2);
-          dequant_fp8_rowgroup(FA_KVBUF((K + 1) % 3), wave);
-          const RowPair r = row_valid(t + 2, rr);
+          const RowPair r = row_valid(t + 2, read_rows(t + 2));
           request_rows(t + 4);
           creq = gather_req(r, b_cp);
           vq[0] = vq[1];
@@ -876,8 +894,17 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         __builtin_amdgcn_sched_barrier(0);
 
         // PV(t): dims 128*wave.. of all 128 rows, 64 MFMAs; P^T read two row
-        // tiles ahead
+        // tiles ahead.  fp8: this wave's row-group of tile t+1 becomes bf16
+        // here, one 16-byte chunk per lane between each row tile's MFMAs
+        // (which it runs beside); its raw copies, requested during QK(t-1),
+        // have had until now to land.  It is read from step t+1 on.
         {
+          Fp8Codes dq;
+          if constexpr (kMode == kSparseFp8) {
+            wait_vmem<kFp8Copies + 1>();  // tile t+2's copies and rows may be in flight
+            __builtin_amdgcn_sched_barrier(0);
+            dq = fp8_load(FA_KVBUF((K + 1) % 3), wave);
+          }
           bf16x8 pb[2];
           auto p_read = [&](int rt) -> bf16x8 {
             return *reinterpret_cast<const bf16x8*>(sm.p + lo.p + rt * 1024);
@@ -892,9 +919,53 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
                 copy_block(creq, IntTag<kRowTiles>{});
             }
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kMode == kSparseFp8) {
+              // one chunk of the conversion, a few instructions after each
+              // MFMA (fenced in place), so that it issues while the MFMAs run
+              constexpr int I = rt / 2, H = rt % 2;
+              const unsigned int w0 = dq.code[I][2 * H], w1 = dq.code[I][2 * H + 1];
+              floatx2 f[4];
+              uintx4 o;
+              int off;
+              auto mf = [&](int dt) {
+                mfma16_aacc(va[dt], pb[rt % 2], acc[dt][rt]);
+                __builtin_amdgcn_sched_barrier(0);
+              };
+              auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+              mf(0);
+              f[0] = fp8x2_to_f32<false>(w0);
+              f[1] = fp8x2_to_f32<true>(w0);
+              fence();
+              mf(1);
+              f[2] = fp8x2_to_f32<false>(w1);
+              f[3] = fp8x2_to_f32<true>(w1);
+              fence();
+              mf(2);
 #pragma unroll
-            for (int dt = 0; dt < kDimTiles; ++dt) mfma16_aacc(va[dt], pb[rt % 2], acc[dt][rt]);
-            __builtin_amdgcn_sched_barrier(0);
+              for (int j = 0; j < 2; ++j) f[j] = floatx2{f[j][0] * dq.scale, f[j][1] * dq.scale};
+              fence();
+              mf(3);
+#pragma unroll
+              for (int j = 2; j < 4; ++j) f[j] = floatx2{f[j][0] * dq.scale, f[j][1] * dq.scale};
+              fence();
+              mf(4);
+              o[0] = pack_bf16x2(f[0][0], f[0][1]);
+              o[1] = pack_bf16x2(f[1][0], f[1][1]);
+              fence();
+              mf(5);
+              o[2] = pack_bf16x2(f[2][0], f[2][1]);
+              o[3] = pack_bf16x2(f[3][0], f[3][1]);
+              off = fp8_store_off<I, H>(dq);
+              fence();
+              mf(6);
+              *reinterpret_cast<uintx4*>(FA_KVBUF((K + 1) % 3) + off) = o;
+              fence();
+              mf(7);
+            } else {
+#pragma unroll
+              for (int dt = 0; dt < kDimTiles; ++dt) mfma16_aacc(va[dt], pb[rt % 2], acc[dt][rt]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
           });
         }
       };
