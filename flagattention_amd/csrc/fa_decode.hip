@@ -653,7 +653,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         // Q is requested beside the rows of tiles 0 and 1, and both are
         // waited for before the first copies: the compiler then knows Q has
         // landed (it does not see the row and tile loads, so a wait for part
-        // of Q would come out as a full wait inside the loop)
+        // of Q would come out as a full wait inside the loop).  (Requesting Q
+        // behind the first copies instead measured 3% slower.)
         if (with_q) load_q();  // uniform
         wait_vmem<0>();
         const RowPair r0 = row_valid(0, read_rows(0)), r1 = row_valid(1, read_rows(1));
@@ -712,7 +713,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         } else if constexpr (kMode == kDense) {
           wait_vmem<kCopiesPerWave>();
         }
-        barrier();
+        // the step's own set-up (this wave's rows, pages and offsets) before
+        // the barrier, whose wait it then overlaps
         const unsigned int vm = vq[0];
         LaneOffsets lo = lane_offsets();
         lane_offsets_vp(lo);
@@ -736,6 +738,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           vq[0] = vq[1];
           vq[1] = row_mask(r);
         }
+        barrier();
         __builtin_amdgcn_sched_barrier(0);
 
         // QK(t): S of rows 32*wave.. for the 32 tokens, 72 MFMAs in four
