@@ -11,7 +11,7 @@
 // tile goes through two phases separated by work-group barriers:
 //   1. S = Q K^T and the softmax, split by rows: wave w owns rows 32w..32w+31
 //      (its Q^T operand, 32 rows x 576 dims, stays in VGPRs; sparse decode
-//      keeps 11 of its 36 16-byte pieces in LDS), computes their
+//      keeps 4 of its 36 16-byte pieces in LDS), computes their
 //      S on MFMA 16x16x32 bf16 in four independent accumulator chains and
 //      writes P (bf16, against a fixed per-row reference, below) to LDS;
 //   2. O^T += V^T P^T on MFMA 16x16x32 bf16, split by value dims: wave w owns
@@ -36,6 +36,16 @@
 //
 // Unsplit sequences are normalised and written as bf16 out / fp32 lse; split
 // ones write (o bf16, lse fp32) partials for fa_mla_combine.
+//
+// Waits: every tile copy is an LDS-destination load counted in vmcnt, and the
+// kernel waits for them with explicit counts (the same number of copies per
+// tile in every lane).  The sparse copies are issued from inline asm: the
+// compiler would book the builtin as a flat access that may also be pending
+// on the LDS counter and then wait for every LDS read with lgkmcnt(0).  Since
+// it does not see those loads, the sparse loops load nothing it tracks: the
+// row ids of a tile go through an LDS ring, and Q is retired with a full wait
+// before the first copies.  No value is spilled inside the loops (a reload is
+// a vmem wait that would drain every copy in flight).
 //
 // LDS tile layout: the 32 x 72 grid of 16-byte chunks (row r, logical chunk
 // k) is stored as 4 row-groups x 9 chunk-groups of 1 KB blocks.  Block

@@ -219,6 +219,28 @@ def test_sparse_wide_score_spread():
     assert_close(out, lse, ref_out, ref_lse, low)
 
 
+def test_sparse_fp8_wide_score_spread():
+    """The second pass through the fp8 pipeline (rows converted in place a step ahead):
+    a planted fp8 row of 1.5s (scale 1, rope 1.5) scores ~90 log2 units above the first
+    tile's row max, in a late tile of sequence 0 only."""
+    need_gpu()
+    say("sparse fp8 wide score spread")
+    lens = [3000, 3000]
+    q, kc, bt, ld = orc.make_dense_inputs(2, 128, 1, lens, seed=80, scale=0.1)
+    q.fill_(1.0)
+    kc8 = orc.make_fp8_cache(kc.shape[0], seed=81, lat_scale=0.1)
+    idx = orc.make_sparse_indices(2, 1, 1024, lens, seed=82, invalid_frac=0.0)
+    j = int(idx[0, 0, 900])  # index slot 900: tile 28 of 32
+    row = orc.fp8_rows_quantize(torch.full((1, 512), 1.5),
+                                torch.full((1, 64), 1.5, dtype=torch.bfloat16), torch.ones((1, 4)))
+    kc8[int(bt[0, j // 64]), j % 64, 0, :] = row[0]
+    out, lse = run_sparse(q, kc8, bt, ld, idx, SCALE, True)
+    ref_out, ref_lse, low, low_lse = sparse_refs(q, kc8, bt, ld, idx, SCALE, True)
+    assert float(ref_lse[0].min()) > 60.0  # the planted key dominates sequence 0
+    assert float(ref_lse[1].max()) < 30.0  # sequence 1 keeps its first-tile reference
+    assert_close(out, lse, ref_out, ref_lse, low, low_lse)
+
+
 # ---------------------------------------------------------------- sparse
 
 @pytest.mark.parametrize("name,fp8", [("sparse_bf16.npz", False), ("sparse_fp8.npz", True)])
