@@ -235,10 +235,7 @@ __device__ inline int fp8_store_off(const Fp8Codes& c) {
   return c.base + 16 * ((2 * ((I + c.eh) & 3) + H) ^ c.r);
 }
 template <int I, int H>  // piece I of the four, half H: 8 codes -> one 16-byte bf16 chunk
-__device__ inline void fp8_store(unsigned char* buf, int wave, const Fp8Codes& c) {
-  const int lane = fresh_lane();
-  const int r = lane >> 3, e = lane & 7;
-  const int m = (I + (e >> 1)) & 3;
+__device__ inline void fp8_store(unsigned char* buf, const Fp8Codes& c) {
   const unsigned int w0 = c.code[I][2 * H], w1 = c.code[I][2 * H + 1];
   floatx2 a = fp8x2_to_f32<false>(w0), b = fp8x2_to_f32<true>(w0);
   floatx2 d = fp8x2_to_f32<false>(w1), f = fp8x2_to_f32<true>(w1);
@@ -247,13 +244,13 @@ __device__ inline void fp8_store(unsigned char* buf, int wave, const Fp8Codes& c
   o[1] = pack_bf16x2(b[0] * c.scale, b[1] * c.scale);
   o[2] = pack_bf16x2(d[0] * c.scale, d[1] * c.scale);
   o[3] = pack_bf16x2(f[0] * c.scale, f[1] * c.scale);
-  *reinterpret_cast<uintx4*>(buf + tile_off(8 * wave + r, 8 * e + 2 * m + H)) = o;
+  *reinterpret_cast<uintx4*>(buf + fp8_store_off<I, H>(c)) = o;
 }
 __device__ inline void dequant_fp8_rowgroup(unsigned char* buf, int wave) {
   const Fp8Codes c = fp8_load(buf, wave);
   static_for<8>([&](auto pt) {
     constexpr int P = decltype(pt)::value;
-    fp8_store<P / 2, P % 2>(buf, wave, c);
+    fp8_store<P / 2, P % 2>(buf, c);
   });
 }
 
