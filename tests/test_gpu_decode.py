@@ -49,6 +49,16 @@ def _t(a):
     # batch / part limits; p * W passes 2^32 (the block total itself stays an int32)
     ([(i * 2654435761) % 2**25 for i in range(4096)], 1024, 0),
     ([3000], 1024, 0),
+    # either side of the one-wave launches' limits (B <= 128 and P <= 256; B <= 256
+    # and P <= 1024), with empty sequences and more parts than blocks
+    ([(i * 7919) % 9000 if i % 5 else 0 for i in range(128)], 256, 0),
+    ([(i * 7919) % 9000 if i % 5 else 0 for i in range(129)], 256, 0),
+    ([(i * 7919) % 9000 if i % 7 else 0 for i in range(256)], 1000, 0),
+    ([(i * 7919) % 9000 if i % 7 else 0 for i in range(257)], 1000, 0),
+    ([1 + (i * 31) % 200 for i in range(100)], 1024, 0),
+    ([0] * 40 + [70] + [0] * 40, 255, 0),
+    ([0] * 200, 300, 2048),
+    ([1] * 128, 256, 100),
 ])
 def test_metadata_kernel_matches_spec(lens, parts, topk):
     need_gpu()
