@@ -107,11 +107,14 @@ void mla_combine_kernel(
   const float ninf = -__builtin_inff();
   const float* lrow = lse_accum + static_cast<long long>(s0) * rows + row;  // stride rows
   const bf16* orows = o_accum + (static_cast<long long>(s0) * rows + row) * kDv + lane * 8;
-  if (ns > 1 && ns <= 8) {  // uniform
-    if (ns <= 4) {
-      combine_small<4>(orows, lrow, ns, rows, orow, lse_out, lane);
-    } else {
-      combine_small<8>(orows, lrow, ns, rows, orow, lse_out, lane);
+  // (uniform) N = 2, 4 or 8: exact counts for every ns would cost the kernel
+  // its 64-VGPR budget (the instances share one register allocation)
+  if (ns > 1 && ns <= 8) {
+    switch (ns) {
+      case 2: combine_small<2>(orows, lrow, ns, rows, orow, lse_out, lane); break;
+      case 3:
+      case 4: combine_small<4>(orows, lrow, ns, rows, orow, lse_out, lane); break;
+      default: combine_small<8>(orows, lrow, ns, rows, orow, lse_out, lane); break;
     }
     return;
   }
