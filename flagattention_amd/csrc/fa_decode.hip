@@ -706,8 +706,15 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       }
 
       // ---- step t: QK(t), softmax(t) -> P | PV(t) ----
-      auto step = [&](const int t, auto tag) {
+      // ctag bit 0: the step requests tile t+2 (and its rows / page); bit 1:
+      // the step before it did.  The steps after the last whole round of
+      // three request nothing (their tiles t+2 lie past the end); in them
+      // the requests' addresses, computed ahead and spilled, were reloaded
+      // before every copy, each reload a vmcnt(0) behind the copy before.
+      auto step = [&](const int t, auto tag, auto ctag) {
         constexpr int K = decltype(tag)::value;  // t % 3
+        constexpr bool kIssue = (decltype(ctag)::value & 1) != 0;
+        constexpr bool kPrevIssued = (decltype(ctag)::value & 2) != 0;
         unsigned char* const b_cur = FA_KVBUF(K);
         unsigned char* const b_cp = FA_KVBUF((K + 2) % 3);
         // this wave's copies of tile t landed (those of t+1 may be in flight),
@@ -715,7 +722,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         // (t+2) % 3.  fp8: tile t was converted during PV(t-1) by the waves
         // that loaded it, after a wait that also covered the rows of tile t+2,
         // so only the barrier is needed.
-        if constexpr (kMode == kSparseBf16) {
+        if constexpr (kMode != kSparseFp8 && !kPrevIssued) {
+          wait_vmem<0>();  // nothing of tile t+1 was requested after tile t
+        } else if constexpr (kMode == kSparseBf16) {
           wait_vmem<kCopiesPerWave + 1>();  // also the rows of tile t+2 (one load)
         } else if constexpr (kMode == kDense) {
           wait_vmem<kCopiesPerWave>();
@@ -726,7 +735,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         LaneOffsets lo = lane_offsets();
         lane_offsets_vp(lo);
         CopyReq creq;  // tile t+2, issued block by block during QK(t) or PV(t)
-        if constexpr (kMode == kDense) {
+        if constexpr (!kIssue) {
+          vq[0] = vq[1];
+          vq[1] = 0u;
+        } else if constexpr (kMode == kDense) {
           unsigned int m;
           creq = dense_req(t + 2, page_of(t + 2, page_q), b_cp, &m);
           page_q = load_page(t + 3);  // ahead of tile t+2's copies
@@ -767,7 +779,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
               ka[(kq + kPre) % kRing][0] = k_read(lo, b_cur, kq + kPre, 0);
             }
             const bf16x8 q0 = q_op(2 * kq), q1 = q_op(2 * kq + 1);
-            if constexpr (!kCopiesInPv && (kq & 1) == 0 && (kq >> 1) < kCopies)
+            if constexpr (kIssue && !kCopiesInPv && (kq & 1) == 0 && (kq >> 1) < kCopies)
               copy_block(creq, IntTag<(kq >> 1)>{});
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 a0 = ka[kq % kRing][0], a1 = ka[kq % kRing][1];
@@ -911,7 +923,11 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
         {
           Fp8Codes dq;
           if constexpr (kMode == kSparseFp8) {
-            wait_vmem<kFp8Copies + 1>();  // tile t+2's copies and rows may be in flight
+            if constexpr (kIssue) {
+              wait_vmem<kFp8Copies + 1>();  // tile t+2's copies and rows may be in flight
+            } else {
+              wait_vmem<0>();
+            }
             __builtin_amdgcn_sched_barrier(0);
             dq = fp8_load(FA_KVBUF((K + 1) % 3), wave);
           }
@@ -923,7 +939,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
           static_for<kRowTiles>([&](auto rtt) {
             constexpr int rt = decltype(rtt)::value;
             if constexpr (rt + 1 < kRowTiles) pb[(rt + 1) % 2] = p_read(rt + 1);
-            if constexpr (kCopiesInPv) {
+            if constexpr (kIssue && kCopiesInPv) {
               if constexpr (rt < kCopies) copy_block(creq, IntTag<rt>{});
               if constexpr (rt == kRowTiles - 1 && kCopies > kRowTiles)
                 copy_block(creq, IntTag<kRowTiles>{});
@@ -984,13 +1000,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       // buffers the same on every iteration).
       int t = 0;
       for (; t + 3 <= ntiles; t += 3) {
-        step(t, IntTag<0>{});
-        step(t + 1, IntTag<1>{});
-        step(t + 2, IntTag<2>{});
+        step(t, IntTag<0>{}, IntTag<3>{});
+        step(t + 1, IntTag<1>{}, IntTag<3>{});
+        step(t + 2, IntTag<2>{}, IntTag<3>{});
       }
       if (t < ntiles) {
-        step(t, IntTag<0>{});
-        if (t + 1 < ntiles) step(t + 1, IntTag<1>{});
+        step(t, IntTag<0>{}, IntTag<2>{});
+        if (t + 1 < ntiles) step(t + 1, IntTag<1>{}, IntTag<0>{});
       }
       wait_vmem<0>();  // requests for tiles past the end land before LDS is reused
       if (pass > 0) {
