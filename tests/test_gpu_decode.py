@@ -291,6 +291,33 @@ def test_sparse_random(fp8, topk, parts):
     assert_close(out, lse, *sparse_refs(q, kc, bt, ld, idx, SCALE, fp8))
 
 
+@pytest.mark.parametrize("parts", [None, 1, 5])
+def test_dense_segments_of_every_tile_count(parts):
+    """Segments of 1..7 tiles of 32 tokens, full and one token into the next tile: every
+    count modulo the three-buffer round (the steps after the last whole round request no
+    tiles)."""
+    need_gpu()
+    lens = [1, 32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193]
+    say(f"dense tile counts parts={parts}")
+    q, kc, bt, ld = orc.make_dense_inputs(len(lens), 128, 1, lens, seed=31, scale=1.0,
+                                          extra_blocks=2)
+    out, lse, _, _ = run_dense(q, kc, bt, ld, SCALE, False, parts)
+    assert_close(out, lse, *dense_refs(q, kc, bt, ld, SCALE, False))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("topk,parts", [(32, None), (64, 1), (96, None), (128, 1), (160, None),
+                                        (160, 1)])
+def test_sparse_segments_of_every_tile_count(fp8, topk, parts):
+    """Sparse segments of 1..5 tiles (top-k 32..160): every count modulo the three-buffer
+    round, with and without splits."""
+    need_gpu()
+    say(f"sparse tile counts fp8={fp8} topk={topk} parts={parts}")
+    q, kc, bt, ld, idx = sparse_random_inputs(fp8, topk)
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8, parts)
+    assert_close(out, lse, *sparse_refs(q, kc, bt, ld, idx, SCALE, fp8))
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("h_q,s_q,topk", [(100, 2, 300), (256, 1, 500), (16, 3, 64)])
 def test_sparse_head_and_token_shapes(fp8, h_q, s_q, topk):
