@@ -868,8 +868,11 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #pragma unroll
             for (int i = 0; i < 4; ++i) sv[4 * tt + i] = sacc[tt][rt][i] * scale_log2;
           if (partial) {
+            // sparse: a slot's position is not a token position, so only the
+            // tile's row mask applies (-1 and ids past the length, set by the
+            // row translation); the length / causal limit is dense-only
             const unsigned int vmg = vm >> (4 * G);
-            const int lim = row_limit(rt) - kTileRows * t - 4 * G;
+            const int lim = kMode == kDense ? row_limit(rt) - kTileRows * t - 4 * G : kTileRows;
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll

@@ -346,6 +346,28 @@ def test_dense_multi_row_block(h_q, s_q, causal):
     assert_close(out, lse, *dense_refs(q, kc, bt, ld, SCALE, causal))
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_sparse_valid_indices_past_the_cache_length(fp8):
+    """A top-k list longer than the cache with its valid ids scattered over every slot:
+    slot positions are not token positions, so slots at or past the cache length hold
+    keys like any other (only -1 and ids >= the length are masked)."""
+    need_gpu()
+    lens = [100, 37]
+    topk = 256
+    q, kc, bt, ld = orc.make_dense_inputs(2, 128, 1, lens, seed=12, scale=1.0, extra_blocks=1)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=13, lat_scale=1.0)
+    gen = torch.Generator().manual_seed(14)
+    idx = torch.full((2, 1, topk), -1, dtype=torch.int32)
+    for b, n in enumerate(lens):
+        slots = torch.randperm(topk, generator=gen)[:n]
+        idx[b, 0, slots] = torch.randperm(n, generator=gen).to(torch.int32)
+    idx[0, 0, 7] = 100  # == the cache length: masked
+    assert int((idx[0, 0, lens[0]:] >= 0).sum()) > 30  # valid ids past slot len
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8)
+    assert_close(out, lse, *sparse_refs(q, kc, bt, ld, idx, SCALE, fp8))
+
+
 def test_sparse_all_masked_row():
     need_gpu()
     q, kc, bt, ld = orc.make_dense_inputs(2, 64, 1, [300, 300], seed=4)
