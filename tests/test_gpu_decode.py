@@ -49,8 +49,8 @@ def _t(a):
     # batch / part limits; p * W passes 2^32 (the block total itself stays an int32)
     ([(i * 2654435761) % 2**25 for i in range(4096)], 1024, 0),
     ([3000], 1024, 0),
-    # either side of the one-wave launches' limits (B <= 128 and P <= 256; B <= 256
-    # and P <= 1024), with empty sequences and more parts than blocks
+    # batches of 128 / 129 / 256 / 257 with empty sequences, short sequences under many
+    # parts (more parts than blocks), all-empty and tiny top-k batches
     ([(i * 7919) % 9000 if i % 5 else 0 for i in range(128)], 256, 0),
     ([(i * 7919) % 9000 if i % 5 else 0 for i in range(129)], 256, 0),
     ([(i * 7919) % 9000 if i % 7 else 0 for i in range(256)], 1000, 0),
@@ -366,6 +366,34 @@ def test_sparse_valid_indices_past_the_cache_length(fp8):
     assert int((idx[0, 0, lens[0]:] >= 0).sum()) > 30  # valid ids past slot len
     out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8)
     assert_close(out, lse, *sparse_refs(q, kc, bt, ld, idx, SCALE, fp8))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_sparse_duplicate_ids(fp8):
+    """Repeated ids count once per slot.  Row 0 lists one id in all 128 slots: its
+    attention is that key's value exactly, with lse = its score + ln 128; row 1 repeats
+    a few ids among distinct ones (checked against the oracle)."""
+    need_gpu()
+    lens = [300, 300]
+    topk = 128
+    q, kc, bt, ld = orc.make_dense_inputs(2, 64, 1, lens, seed=21, scale=1.0, extra_blocks=1)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=22, lat_scale=1.0)
+    idx = orc.make_sparse_indices(2, 1, topk, lens, seed=23, invalid_frac=0.0)
+    idx[0] = 5
+    idx[1, 0, 64:96] = idx[1, 0, :32]
+    out, lse = run_sparse(q, kc, bt, ld, idx, SCALE, fp8)
+    ref_out, ref_lse, low, low_lse = sparse_refs(q, kc, bt, ld, idx, SCALE, fp8)
+    assert_close(out, lse, ref_out, ref_lse, low, low_lse)
+    # closed form for row 0: the one key of id 5 (physical row through the table)
+    row = int(bt[0, 0]) * 64 + 5
+    flat = kc.reshape(-1, kc.shape[-1])
+    kv = orc.fp8_rows_dequant(flat[row:row + 1]) if fp8 else flat[row:row + 1].float()
+    kv = kv.to(torch.bfloat16).float()  # the MFMA input (fp8 rows become bf16 on chip)
+    score = (q[0, 0].float() @ kv[0]) * SCALE
+    torch.testing.assert_close(lse[0, :, 0], score + math.log(topk), atol=2e-2, rtol=0)
+    torch.testing.assert_close(out[0, 0].float(), kv[0, :512].expand(64, 512), atol=2e-2,
+                               rtol=1e-2)
 
 
 def test_sparse_all_masked_row():
