@@ -878,8 +878,17 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 const int c = 16 * tt + i;
-                const bool ok = ((vmg >> c) & 1u) && c < lim;
-                sv[4 * tt + i] = ok ? sv[4 * tt + i] : ninf;
+                if constexpr (kMode == kDense) {
+                  const bool ok = ((vmg >> c) & 1u) && c < lim;
+                  sv[4 * tt + i] = ok ? sv[4 * tt + i] : ninf;
+                } else {
+                  // bit c as 0 / all ones (signed one-bit extract), then a
+                  // bitwise select: two VALU per score, no condition mask
+                  const unsigned int m = static_cast<unsigned int>(
+                      __builtin_amdgcn_sbfe(static_cast<int>(vmg), c, 1));
+                  sv[4 * tt + i] = __uint_as_float((m & __float_as_uint(sv[4 * tt + i])) |
+                                                   (~m & __float_as_uint(ninf)));
+                }
               }
           }
           // this lane's running max: the overflow check and the second
