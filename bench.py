@@ -437,6 +437,96 @@ def run_topk(args) -> None:
     print(json.dumps(rec), flush=True)
 
 
+KVC_WORKLOADS = {
+    "kvcache": dict(name="kvcache_write_bf16_t131072", tokens=131072, fp8=False, seed=14),
+    "kvcache_fp8": dict(name="kvcache_write_fp8_t131072", tokens=131072, fp8=True, seed=15),
+}
+KVC_METRIC = "MLA cache write µs/step + achieved HBM GB/s (% of roofline)"
+
+
+def run_kvcache(args) -> None:
+    """Cache write path bench (concat_and_cache_mla): a prefill-sized batch of new tokens
+    (latent + rope, bf16) written into shuffled pages of the paged cache; two input copies
+    rotated.  A step is one launch, timed with events around it on its stream."""
+    import flag_attn
+
+    spec = KVC_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(spec["seed"])
+    t, fp8 = spec["tokens"], spec["fp8"]
+    pages = t // 64
+    row = 656 if fp8 else 576
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    cache = torch.zeros((pages, 64, 1, row), dtype=dt, device=dev)
+    lat = [torch.randn((t, 512), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
+    rope = [torch.randn((t, 64), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
+    perm = torch.randperm(pages, generator=gen, device=dev).to(torch.int32)
+    tok = torch.arange(t, device=dev, dtype=torch.int32)
+    slots = perm[tok // 64] * 64 + tok % 64
+
+    def step(i):
+        flag_attn.concat_and_cache_mla(lat[i % 2], rope[i % 2], cache, slots, fp8)
+
+    t_warm = time.perf_counter()
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    settle_steps = 0
+    while time.perf_counter() - t_warm < SETTLE_S:
+        for _ in range(20):
+            step(settle_steps)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_warm
+    every = max(1, min(EVENT_EVERY, args.steps // MIN_EVENT_LAUNCHES))
+    stream = torch.cuda.current_stream()
+    evs = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for i in range(0, args.steps, every)}
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev = evs.get(i)
+        if ev:
+            ev[0].record(stream)
+        step(i)
+        if ev:
+            ev[1].record(stream)
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) / args.steps * 1e6
+    dec = sorted(s.elapsed_time(e) for s, e in evs.values())
+    k_us = sum(dec) / len(dec) * 1e3
+    # tokens read (latent + rope, bf16), rows written, one int32 slot per token
+    nbytes = t * (1152 + (656 if fp8 else 1152) + 4)
+    gbs = nbytes / (k_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import mla_oracle as orc
+        n = 4096
+        sample_cache = torch.zeros((n // 64, 64, 1, row), dtype=dt)
+        sl, sr = lat[0][:n].cpu(), rope[0][:n].cpu()
+        sslots = torch.arange(n, dtype=torch.int64)
+        t1 = time.perf_counter()
+        orc.kvcache_write_ref(sample_cache, sl, sr, sslots, fp8)
+        t_cpu = time.perf_counter() - t1
+        cpu = {"value": round(t_cpu * (t / n) * 1e6, 1), "unit": "µs/step",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{n} of {t} tokens (oracle writer), scaled x{t // n} to the full step"}
+    rec = {
+        "metric": KVC_METRIC, "value": round(us_step, 2), "unit": "µs/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "settle_s": round(settle_s, 3),
+        "settle_steps": settle_steps, "ms_per_step": round(us_step / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3" if fp8 else "bf16", "data": "synthetic",
+        "config": {"workload": spec["name"], "tokens": t, "pages": pages,
+                   "row_bytes": 656 if fp8 else 1152},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "mla_kvcache_write_kernel", "kernel_launches_timed": len(dec),
+                     "kernel_us_mean": round(k_us, 2), "bytes_per_launch": nbytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -444,7 +534,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--workload", default="dense",
                     choices=["dense", "skew", "sparse", "sparse_fp8"] + list(GQA_WORKLOADS)
-                    + list(TOPK_WORKLOADS))
+                    + list(TOPK_WORKLOADS) + list(KVC_WORKLOADS))
     ap.add_argument("--copies", type=int, default=2, help="rotated KV pools (cache defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-calibrate", action="store_true",
@@ -463,6 +553,9 @@ def main() -> None:
         return
     if args.workload in TOPK_WORKLOADS:
         run_topk(args)
+        return
+    if args.workload in KVC_WORKLOADS:
+        run_kvcache(args)
         return
 
     import flag_attn.mla as fa

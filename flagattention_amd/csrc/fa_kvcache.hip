@@ -5,8 +5,8 @@
 //   bytes [512, 528)  one fp32 scale per 128 dims, scale = amax / 448 (1 for
 //                     an all-zero tile), code = e4m3(clamp(x / scale, +-448)),
 //   bytes [528, 656)  the 64 rope dims in bf16.
-// One wave per token: lane l holds latent dims 8l..8l+7; the 16 lanes of a
-// 128-dim tile reduce its amax with four lane exchanges.
+// Lane l holds latent dims 8l..8l+7 of a token; the 16 lanes of a 128-dim
+// tile reduce its amax with four lane exchanges.
 //
 // The reference has no cache writer (its tests fill caches in place); the
 // row formats are the ones fa_mla_decode_dense / fa_mla_decode_sparse read.
@@ -20,46 +20,62 @@ __device__ inline unsigned int fp8x2(float a, float b) {
   return static_cast<unsigned int>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xFFFFu;
 }
 
+// A wave writes kTokPerWave consecutive tokens: every load (the tokens'
+// slots through the scalar unit -- they are wave-uniform -- and their latent
+// and rope vectors, at clamped in-bounds addresses) is issued before any
+// store, so a wave waits for one memory round trip instead of one per token.
+constexpr int kTokPerWave = 4;
+
 __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
     const bf16* __restrict__ kv_c, long long kv_c_stride, const bf16* __restrict__ k_pe,
     long long k_pe_stride, const long long* __restrict__ slot_mapping, int num_tokens,
     unsigned char* __restrict__ cache, long long block_stride, long long row_stride,
     long long num_rows, int fp8) {
-  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tok >= num_tokens) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tok0 = (blockIdx.x * 4 + wave) * kTokPerWave;
+  if (tok0 >= num_tokens) return;
   const int lane = threadIdx.x & 63;
-  const long long slot = slot_mapping[tok];
-  if (slot < 0 || slot >= num_rows) return;  // padding tokens / slots outside the cache
-  unsigned char* row = cache + (slot >> 6) * block_stride + (slot & 63) * row_stride;
-  const bf16x8 x = *reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane);
-  bf16x8 pe{};
-  if (lane < 8) pe = *reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane);
-  if (!fp8) {
-    *reinterpret_cast<bf16x8*>(row + 16 * lane) = x;
-    if (lane < 8) *reinterpret_cast<bf16x8*>(row + 1024 + 16 * lane) = pe;
-    return;
-  }
-  float f[8];
-  float amax = 0.f;
+  long long slot[kTokPerWave];
+  bf16x8 x[kTokPerWave], pe[kTokPerWave];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    f[i] = static_cast<float>(x[i]);
-    amax = fmaxf(amax, fabsf(f[i]));
+  for (int j = 0; j < kTokPerWave; ++j) {
+    const int tok = min(tok0 + j, num_tokens - 1);
+    slot[j] = tok0 + j < num_tokens ? slot_mapping[tok] : -1;
+    x[j] = *reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane);
+    pe[j] = bf16x8{};
+    if (lane < 8) pe[j] = *reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane);
   }
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-  const float scale = amax > 0.f ? amax / 448.f : 1.f;
-  uintx2 codes;
+  for (int j = 0; j < kTokPerWave; ++j) {
+    if (slot[j] < 0 || slot[j] >= num_rows) continue;  // padding tokens / slots outside the cache
+    unsigned char* row = cache + (slot[j] >> 6) * block_stride + (slot[j] & 63) * row_stride;
+    if (!fp8) {
+      *reinterpret_cast<bf16x8*>(row + 16 * lane) = x[j];
+      if (lane < 8) *reinterpret_cast<bf16x8*>(row + 1024 + 16 * lane) = pe[j];
+      continue;
+    }
+    float f[8];
+    float amax = 0.f;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    float v[4];
+    for (int i = 0; i < 8; ++i) {
+      f[i] = static_cast<float>(x[j][i]);
+      amax = fmaxf(amax, fabsf(f[i]));
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(f[4 * w + i] / scale, -448.f), 448.f);
-    codes[w] = fp8x2(v[0], v[1]) | (fp8x2(v[2], v[3]) << 16);
+    for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float scale = amax > 0.f ? amax / 448.f : 1.f;
+    uintx2 codes;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(f[4 * w + i] / scale, -448.f), 448.f);
+      codes[w] = fp8x2(v[0], v[1]) | (fp8x2(v[2], v[3]) << 16);
+    }
+    *reinterpret_cast<uintx2*>(row + 8 * lane) = codes;
+    if ((lane & 15) == 0) *reinterpret_cast<float*>(row + 512 + 4 * (lane >> 4)) = scale;
+    if (lane < 8) *reinterpret_cast<bf16x8*>(row + 528 + 16 * lane) = pe[j];
   }
-  *reinterpret_cast<uintx2*>(row + 8 * lane) = codes;
-  if ((lane & 15) == 0) *reinterpret_cast<float*>(row + 512 + 4 * (lane >> 4)) = scale;
-  if (lane < 8) *reinterpret_cast<bf16x8*>(row + 528 + 16 * lane) = pe;
 }
 
 }  // namespace
@@ -83,7 +99,7 @@ extern "C" int fa_mla_kvcache_write(const void* kv_c, int64_t kv_c_stride, const
   FA_CHECK_ARG(num_kv_blocks >= 1, "num_kv_blocks %lld < 1", static_cast<long long>(num_kv_blocks));
   FA_CHECK_ARG(kv_row_stride >= (fp8 ? FA_MLA_FP8_ROW_BYTES : 2 * FA_MLA_D_QK),
                "cache row stride %lld smaller than the row", static_cast<long long>(kv_row_stride));
-  const dim3 grid(static_cast<unsigned>((num_tokens + 3) / 4));
+  const dim3 grid(static_cast<unsigned>(fa::cdiv(num_tokens, 4 * fa::kTokPerWave)));
   hipLaunchKernelGGL(fa::mla_kvcache_write_kernel, grid, dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const fa::bf16*>(kv_c),
                      static_cast<long long>(kv_c_stride), static_cast<const fa::bf16*>(k_pe),
