@@ -460,8 +460,9 @@ def run_kvcache(args) -> None:
     cache = torch.zeros((pages, 64, 1, row), dtype=dt, device=dev)
     lat = [torch.randn((t, 512), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
     rope = [torch.randn((t, 64), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
-    perm = torch.randperm(pages, generator=gen, device=dev).to(torch.int32)
-    tok = torch.arange(t, device=dev, dtype=torch.int32)
+    # int64 slots, the usual slot_mapping type (int32 ones are widened per call)
+    perm = torch.randperm(pages, generator=gen, device=dev)
+    tok = torch.arange(t, device=dev, dtype=torch.int64)
     slots = perm[tok // 64] * 64 + tok % 64
 
     def step(i):
