@@ -708,9 +708,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       // ---- step t: QK(t), softmax(t) -> P | PV(t) ----
       // ctag bit 0: the step requests tile t+2 (and its rows / page); bit 1:
       // the step before it did.  The steps after the last whole round of
-      // three request nothing (their tiles t+2 lie past the end); in them
-      // the requests' addresses, computed ahead and spilled, were reloaded
-      // before every copy, each reload a vmcnt(0) behind the copy before.
+      // three request nothing: their tiles t+2 lie past the end, and
+      // issuing those masked copies there makes the compiler compute the
+      // addresses ahead and spill them, each reload a vmcnt(0) behind the
+      // copy before.
       auto step = [&](const int t, auto tag, auto ctag) {
         constexpr int K = decltype(tag)::value;  // t % 3
         constexpr bool kIssue = (decltype(ctag)::value & 1) != 0;
