@@ -396,6 +396,62 @@ def test_sparse_duplicate_ids(fp8):
                                rtol=1e-2)
 
 
+def _padded_views(q, kc, bt, pad_row):
+    """Views with non-default strides over the same values: q with its (s, h) axes
+    stored transposed and padded rows, cache rows padded to pad_row elements, and the
+    block table as a column slice of a wider table."""
+    b, s_q, h_q, d = q.shape
+    qb = torch.zeros((b, h_q, s_q, d + 64), dtype=q.dtype)
+    qb[..., :d] = q.transpose(1, 2)
+    qv = qb[..., :d].transpose(1, 2)
+    kb = torch.zeros(kc.shape[:3] + (pad_row,), dtype=kc.dtype)
+    kb[..., :kc.shape[3]] = kc
+    kv = kb[..., :kc.shape[3]]
+    tb = torch.full((bt.shape[0], bt.shape[1] + 5), -7, dtype=bt.dtype)
+    tb[:, 2:2 + bt.shape[1]] = bt
+    tv = tb[:, 2:2 + bt.shape[1]]
+    assert not qv.is_contiguous() and not kv.is_contiguous() and not tv.is_contiguous()
+    return qb, kb, tb, qv, kv, tv
+
+
+def _dev_view(base, view):
+    """The same view of base, on the GPU (strides kept)."""
+    d = base.to(DEV)
+    return torch.as_strided(d, view.shape, view.stride(), view.storage_offset())
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_strided_inputs(causal):
+    need_gpu()
+    lens = [900, 130, 2000]
+    q, kc, bt, ld = orc.make_dense_inputs(3, 128, 2, lens, seed=41, scale=1.0, extra_blocks=2)
+    qb, kb, tb, qv, kv, tv = _padded_views(q, kc, bt, 640)
+    qd, kd, td = _dev_view(qb, qv), _dev_view(kb, kv), _dev_view(tb, tv)
+    ldd = ld.to(DEV)
+    md, ns = flag_attn.get_mla_metadata(ldd, 2 * 128, 1)
+    out, lse = flag_attn.flash_mla_with_kvcache(qd, kd, td, ldd, 512, md, ns, SCALE, causal)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), lse.cpu(), *dense_refs(q, kc, bt, ld, SCALE, causal))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_sparse_strided_inputs(fp8):
+    need_gpu()
+    lens = [1500, 800]
+    q, kc, bt, ld = orc.make_dense_inputs(2, 128, 1, lens, seed=42, scale=1.0, extra_blocks=1)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=43, lat_scale=1.0)
+    idx = orc.make_sparse_indices(2, 1, 300, lens, seed=44)
+    qb, kb, tb, qv, kv, tv = _padded_views(q, kc, bt, 672 if fp8 else 640)
+    qd, kd, td = _dev_view(qb, qv), _dev_view(kb, kv), _dev_view(tb, tv)
+    ldd = ld.to(DEV)
+    md, ns = flag_attn.get_mla_metadata(ldd, 128, 1, num_heads_q=128, topk=300)
+    out, lse = flag_attn.flash_mla_with_kvcache(qd, kd, td, ldd, 512, md, ns, SCALE, False,
+                                                is_fp8_kvcache=fp8, indices=idx.to(DEV))
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), lse.cpu(), *sparse_refs(q, kc, bt, ld, idx, SCALE, fp8))
+
+
 def test_sparse_all_masked_row():
     need_gpu()
     q, kc, bt, ld = orc.make_dense_inputs(2, 64, 1, [300, 300], seed=4)
