@@ -121,6 +121,9 @@ DENSE_CASES = [
     (3, 16, 2, [65, 7, 200], True, 2),
     (2, 100, 1, [700, 300], False, None),  # h_q not a multiple of 64
     (2, 128, 3, [190, 64], True, None),
+    (2, 64, 2, [300, 1000], False, None),  # several query tokens, no causal mask
+    (2, 1, 1, [500, 70], False, None),  # one query head
+    (3, 8, 4, [33, 512, 2], True, 3),  # four causal tokens, one shorter than s_q
 ]
 
 
