@@ -11,6 +11,8 @@ Restates, on the CPU:
   ``softmax`` -> ``bmm`` (``:58-60``), cast to the cache dtype (``:61``);
 * ``paged_attention_ref`` -- the same arithmetic with the gather vectorised (index tensors
   instead of the token loop); pinned to ``paged_attention_loop`` bit for bit;
+* ``paged_attention_lowp`` -- the same gather with ``testing/flash.py``'s ``upcast=False``
+  arithmetic: the low-precision leg of the three-way rule for the paged sweeps;
 * ``flash_attention_ref`` -- ``src/flag_attn/testing/flash.py:19-84``: GQA by
   ``repeat_interleave`` (``:42-44``), ``S = q k^T * sm_scale`` in the working dtype
   (fp32 with ``upcast=True``, the input dtype otherwise), bottom-right causal mask
@@ -60,9 +62,11 @@ def paged_attention_loop(query, key_cache, value_cache, block_tables, context_le
 
 
 def paged_attention_ref(query, key_cache, value_cache, block_tables, context_lens,
-                        scale) -> torch.Tensor:
-    """``paged_attention_loop`` with the token gather vectorised (same fp32 arithmetic)."""
-    output = torch.empty_like(query)
+                        scale, out_fp32: bool = False) -> torch.Tensor:
+    """``paged_attention_loop`` with the token gather vectorised (same fp32 arithmetic).
+    ``out_fp32=True`` returns the fp32 result before the cast to the cache dtype
+    (``testing/paged.py:61``), the reference point of the three-way accuracy rule."""
+    output = torch.empty(query.shape, dtype=torch.float32) if out_fp32 else torch.empty_like(query)
     h_q = query.shape[1]
     h_kv = value_cache.shape[1]
     group = h_q // h_kv
@@ -81,7 +85,40 @@ def paged_attention_ref(query, key_cache, value_cache, block_tables, context_len
         s = torch.bmm(q.transpose(0, 1).float(), keys.permute(1, 2, 0).float()) * scale
         p = torch.softmax(s, dim=-1)
         out = torch.bmm(p, values.transpose(0, 1).float()).transpose(0, 1)
-        output[i].copy_(out.to(values.dtype).view(h_q, d))
+        output[i].copy_((out if out_fp32 else out.to(values.dtype)).view(h_q, d))
+    return output
+
+
+def paged_attention_lowp(query, key_cache, value_cache, block_tables, context_lens,
+                         scale) -> torch.Tensor:
+    """The paged gather of ``testing/paged.py:37-56`` followed by the ``upcast=False``
+    arithmetic of ``testing/flash.py:47-75`` in the cache dtype: ``S = q k^T`` and
+    ``* scale`` in the dtype, softmax in fp32, ``P`` cast to the dtype, ``P v`` in the
+    dtype.  The reference's paged tests have no such leg (they use ``allclose`` against the
+    fp32 oracle); this one gives the paged sweeps the ``torch_lowp`` side of the rule
+    ``max|hyp - ref| <= 2 max|lowp - ref| + 1e-5`` of
+    ``tests/flag_attn/test_flash_attention.py:119-127``.  Returns the dtype result."""
+    dtype = query.dtype
+    output = torch.empty_like(query)
+    h_q = query.shape[1]
+    h_kv = value_cache.shape[1]
+    group = h_q // h_kv
+    bs = value_cache.shape[2]
+    d = value_cache.shape[3]
+    for i in range(query.shape[0]):
+        n = int(context_lens[i])
+        pos = torch.arange(n)
+        pages = block_tables[i].long()[pos // bs]
+        keys = key_cache[pages, :, pos % bs, :].to(dtype)      # [n, h_kv, d]
+        values = value_cache[pages, :, pos % bs, :].to(dtype)
+        if group > 1:
+            keys = torch.repeat_interleave(keys, group, dim=1)
+            values = torch.repeat_interleave(values, group, dim=1)
+        q = query[i].unsqueeze(1)                               # [h_q, 1, d]
+        s = torch.bmm(q, keys.permute(1, 2, 0).contiguous()) * scale
+        p = torch.softmax(s.float(), dim=-1, dtype=torch.float32)
+        out = torch.bmm(p.to(dtype), values.transpose(0, 1).contiguous())  # [h_q, 1, d]
+        output[i].copy_(out.view(h_q, d))
     return output
 
 

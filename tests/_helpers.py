@@ -17,6 +17,15 @@ LOWP_FACTOR = 2.0
 LOWP_ABS = 1e-5
 
 
+def assert_lowp_rule(hyp, ref, low):
+    """The reference's rule max|hyp - ref| <= 2 max|low - ref| + 1e-5 (ref: the fp32 oracle,
+    low: the oracle in the inputs' low-precision arithmetic)."""
+    e_hyp = float((hyp.float() - ref.float()).abs().max()) if ref.numel() else 0.0
+    e_low = float((low.float() - ref.float()).abs().max()) if ref.numel() else 0.0
+    assert e_hyp <= LOWP_FACTOR * e_low + LOWP_ABS, (
+        f"error {e_hyp:.3e} > {LOWP_FACTOR} x low-precision error {e_low:.3e} + {LOWP_ABS}")
+
+
 def need_gpu():
     assert torch.cuda.is_available(), "GPU tests need an MI355X; none is visible"
 

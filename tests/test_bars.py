@@ -9,8 +9,9 @@ while it accepts the oracle's own answer.
 import pytest
 import torch
 
+from oracle import gqa_oracle as go
 from oracle import mla_oracle as orc
-from tests._helpers import assert_close
+from tests._helpers import assert_close, assert_lowp_rule
 from tests.test_gpu_decode import sparse_random_inputs
 
 SCALE = 192 ** -0.5
@@ -69,3 +70,38 @@ def test_bench_like_dense_bars_reject_wrong_answers():
         bad_lse[b] = l
     _rejects(bad_out.to(torch.bfloat16), bad_lse, ref_out, ref_lse, low)
     _rejects(torch.zeros_like(ref_out).to(torch.bfloat16), ref_lse, ref_out, ref_lse, low)
+
+
+@pytest.mark.parametrize("group,d,bs,max_len,dtype", [
+    (8, 128, 16, 4096, torch.float16), (1, 64, 128, 512, torch.float16),
+    (2, 256, 16, 1500, torch.float16), (8, 128, 16, 1500, torch.bfloat16),
+])
+def test_paged_bars_reject_dropped_and_wrong_pages(group, d, bs, max_len, dtype):
+    """The paged GQA sweep's inputs (uniform(+-D^-0.5), tables drawn with replacement):
+    outputs stay below ~2e-2, so the reference's allclose(atol=2e-3) can pass a kernel
+    that loses the last 16 keys of each sequence.  The three-way rule against the fp32 result
+    and the low-precision leg rejects that, and a wrong page id for the last page, while
+    the oracle's own rounded answer passes both."""
+    gen = torch.Generator().manual_seed(group + d)
+    ns, h, nb = 16, 32, 200
+    s = d ** -0.5
+    lens = torch.randint(1, max_len, (ns,), generator=gen, dtype=torch.int32)
+    lens[0] = max_len
+    q = (torch.rand((ns, h, d), generator=gen) * 2 - 1).mul(s).to(dtype)
+    kc = (torch.rand((nb, h // group, bs, d), generator=gen) * 2 - 1).mul(s).to(dtype)
+    vc = (torch.rand((nb, h // group, bs, d), generator=gen) * 2 - 1).mul(s).to(dtype)
+    bt = torch.randint(0, nb, (ns, -(-max_len // bs)), generator=gen, dtype=torch.int32)
+    ref32 = go.paged_attention_ref(q, kc, vc, bt, lens, s, out_fp32=True)
+    low = go.paged_attention_lowp(q, kc, vc, bt, lens, s)
+    own = go.paged_attention_ref(q, kc, vc, bt, lens, s)
+    assert torch.allclose(own, ref32.to(dtype), atol=2e-3, rtol=1e-5)
+    assert_lowp_rule(own, ref32, low)
+    dropped = go.paged_attention_ref(q, kc, vc, bt, torch.clamp(lens - 16, min=1), s)
+    wrong_bt = bt.clone()
+    for i in range(ns):
+        last = (int(lens[i]) - 1) // bs
+        wrong_bt[i, last] = (wrong_bt[i, last] + 1) % nb
+    wrong = go.paged_attention_ref(q, kc, vc, wrong_bt, lens, s)
+    for bad in (dropped, wrong):
+        with pytest.raises(AssertionError):
+            assert_lowp_rule(bad, ref32, low)

@@ -6,7 +6,8 @@ The sweeps are the reference's own: ``tests/flag_attn/test_paged_attention.py:79
 rtol=1e-5)`` against ``testing.paged_attention``) and
 ``tests/flag_attn/test_flash_attention.py:82-127`` (``test_attention_splitkv``: scale 10,
 BHTD / BTHD strides, fp16 / bf16, causal or not, the rule
-``max|hyp - ref| <= 2 max|torch_lowp - ref| + 1e-5``).  Inputs are seeded here (the
+``max|hyp - ref| <= 2 max|torch_lowp - ref| + 1e-5``).  The paged sweeps apply that rule
+too (against ``gqa_oracle.paged_attention_lowp``) beside the reference's ``allclose``.  Inputs are seeded here (the
 reference's paged tests are not).  Caches are generated on the GPU; the oracle gets CPU
 copies of the pages the block tables name.
 """
@@ -15,7 +16,7 @@ import torch
 
 import flag_attn
 from oracle import gqa_oracle as go
-from tests._helpers import DEV, need_gpu, say
+from tests._helpers import DEV, assert_lowp_rule, need_gpu, say
 
 pytestmark = pytest.mark.gpu
 NUM_BLOCKS = 1000
@@ -58,6 +59,11 @@ def base_paged_attention(num_seqs, num_query_heads, query_group_size, head_size,
     err = float((out.cpu().float() - ref.float()).abs().max())
     say(f"  max |out - ref| = {err:.3e}")
     assert torch.allclose(out.cpu(), ref, atol=2e-3, rtol=1e-5)
+    # the reference's allclose alone passes a kernel that drops a page at these output
+    # sizes; the three-way rule against the fp32 result and the low-precision leg does not
+    ref32 = go.paged_attention_ref(q.cpu(), kc, vc, bt, context_lens, scale, out_fp32=True)
+    low = go.paged_attention_lowp(q.cpu(), kc, vc, bt, context_lens, scale)
+    assert_lowp_rule(out.cpu(), ref32, low)
 
 
 @pytest.mark.parametrize("num_seqs", [1, 32])
@@ -189,3 +195,82 @@ def test_flash_attention_split_kv_and_lse(B, Hq, Hk, M, N, D, causal):
     assert _max_diff(o1, o_ref) <= 2 * _max_diff(o_torch, o_ref) + 1e-5
     assert lse.shape == (B, Hq, M) and lse.dtype == torch.float32
     assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("block_size,group,num_splits", [
+    (8, 1, 0), (8, 1, 3), (24, 1, 3), (24, 4, 0), (48, 8, 5), (48, 2, 1),
+])
+def test_paged_attention_odd_block_sizes(block_size, group, num_splits):
+    """Pages below 16 tokens (the reference allows them at query group 1, paged.py:46) and
+    page sizes that are not powers of two (the kernel divides instead of shifting, and looks
+    pages up per lane), with split starts (next_pow2 partitions) that do not fall on page
+    boundaries."""
+    base_paged_attention(8, 16, group, 64, block_size, 1500, num_splits,
+                         seed=block_size * 10 + group + num_splits)
+
+
+def _oracle_chunked(q, k, v, causal, upcast, chunk=4):
+    """flash_attention_ref over batch slices (the GQA repeat of a whole batch would not fit
+    in host memory at these shapes)."""
+    outs, lses = [], []
+    for b0 in range(0, q.shape[0], chunk):
+        o, lse = go.flash_attention_ref(q[b0:b0 + chunk], k[b0:b0 + chunk], v[b0:b0 + chunk],
+                                        causal, upcast=upcast)
+        outs.append(o)
+        lses.append(lse)
+    return torch.cat(outs), torch.cat(lses)
+
+
+@pytest.mark.parametrize("B, Hq, Hk, M, N, D, causal", [
+    (64, 32, 8, 1, 2048, 128, False),
+    (32, 64, 64, 2, 1500, 64, True),
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("stride_order", ["BHTD", "BTHD"])
+def test_unsplit_contiguous_decode(B, Hq, Hk, M, N, D, causal, dtype, stride_order):
+    """Shapes with enough (sequence, KV head, row block) work-groups to fill the GPU take no
+    split: the decode kernel writes out and lse itself (no combine).  These are the shapes
+    for which the reference's flash_attention takes its _fwd_kernel branch and returns L
+    (flash.py:78-101, split_kv.py:249-251)."""
+    from flagattention_amd import gqa
+    need_gpu()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert gqa.choose_splits(B, Hk, (Hq // Hk) * M, N, cus) == 1
+    q, k, v = _splitkv_inputs(B, Hq, Hk, M, N, D, dtype, stride_order, 1.0, N + M)
+    o_ref, lse_ref = _oracle_chunked(q, k, v, causal, True)
+    o_low, _ = _oracle_chunked(q, k, v, causal, False)
+    o1, lse, _, _, _ = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                                 return_log_normalizer=True)
+    o2 = flag_attn.flash_attention_split_kv(q.to(DEV), k.to(DEV), v.to(DEV), causal)
+    torch.cuda.synchronize()
+    assert o1.dtype == dtype and o1.shape == q.shape
+    assert torch.equal(o1.cpu(), o2.cpu())
+    assert_lowp_rule(o1.cpu(), o_ref, o_low)
+    assert lse.shape == (B, Hq, M) and lse.dtype == torch.float32
+    assert float((lse.cpu() - lse_ref).abs().max()) <= 1e-3
+
+
+@pytest.mark.parametrize("M, N, causal", [
+    (16, 300, False), (64, 700, True), (200, 1000, True), (40, 24, True), (33, 33, True),
+    (17, 5, False),
+])
+def test_flash_attention_many_queries(M, N, causal):
+    """flash_attention with more query positions than a decode step (the reference's
+    forward takes any M, flash.py:269-300): rows of 16 (head, position) pairs per
+    work-group.  Causal with M > N leaves the first M - N positions no key: out 0,
+    lse -inf (the LARGER_M convention of split_kv.py:161-164, flash.py's _fwd_kernel)."""
+    need_gpu()
+    q, k, v = _splitkv_inputs(2, 4, 2, M, N, 64, torch.float16, "BHTD", 1.0, M * 1000 + N)
+    o_ref, lse_ref = go.flash_attention_ref(q, k, v, causal, upcast=True)
+    o_low, _ = go.flash_attention_ref(q, k, v, causal, upcast=False)
+    o, lse, _, _, _ = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                                return_log_normalizer=True)
+    torch.cuda.synchronize()
+    o, lse = o.cpu(), lse.cpu()
+    assert bool(torch.isfinite(o).all())
+    assert_lowp_rule(o, o_ref, o_low)
+    assert torch.equal(torch.isneginf(lse), torch.isneginf(lse_ref))
+    fin = ~torch.isneginf(lse_ref)
+    assert float((lse[fin] - lse_ref[fin]).abs().max()) <= 1e-3
+    if causal and M > N:
+        assert float(o[:, :, : M - N].abs().max()) == 0.0

@@ -177,3 +177,19 @@ def test_c_abi_without_workspace_matches_two_stage():
     assert torch.equal(one.cpu(), two.cpu())
     want = tko.topk_indices_ref(scores.cpu().numpy(), [65536, 40000, 20000], 2048, False)
     assert np.array_equal(one.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("length,topk", [(65536, 8192), (40000, 6000), (20000, 5000)])
+@pytest.mark.parametrize("kind", ["random", "int"])
+def test_two_stage_large_topk(length, topk, kind):
+    """Two-stage plans whose top-k exceeds what the chunk and merge kernels stage in LDS
+    (4096 slots): both then take their range-checked direct-store paths."""
+    from flagattention_amd import _lib
+    need_gpu()
+    assert _lib.load().fa_mla_topk_workspace_bytes(2, 2, length, topk) > 0  # two stages
+    gen = torch.Generator().manual_seed(length + topk)
+    if kind == "random":
+        scores = torch.randn((2, 2, length), generator=gen)
+    else:
+        scores = torch.randint(-4, 4, (2, 2, length), generator=gen).float()
+    _run(scores, [length, length - 3000], topk, causal=True)

@@ -80,3 +80,45 @@ def test_noalloc_rejects_oversized_workspace():
     assert _lib.load().fa_mla_noalloc_scratch_bytes is not None
     with pytest.raises(RuntimeError, match="more than the"):
         decode_noalloc(out, lse, q, kc, bt, lens, md, ns, SCALE)
+
+
+@pytest.mark.parametrize("mode", ["dense", "sparse", "sparse_fp8"])
+def test_noalloc_graph_capture_and_replay(mode):
+    """decode_noalloc captured in a HIP graph (the caller it exists for): replays after the
+    query and cache contents change in place, with eager work and synchronisations between
+    the replays, each bit-identical to an eager flash_mla_with_kvcache on the new data."""
+    need_gpu()
+    say(f"noalloc graph replay: {mode}")
+    lens = [3000, 1000, 4500]
+    fp8 = mode == "sparse_fp8"
+    q, kc, bt, ld = orc.make_dense_inputs(3, 128, 1, lens, seed=80, scale=1.0)
+    if fp8:
+        kc = orc.make_fp8_cache(kc.shape[0], seed=81, lat_scale=1.0)
+    idx = orc.make_sparse_indices(3, 1, 1024, lens, seed=82) if mode != "dense" else None
+    qd, kd, btd, ldd = (t.to(DEV) for t in (q, kc, bt, ld))
+    idd = None if idx is None else idx.to(DEV)
+    md, ns = flag_attn.get_mla_metadata(ldd, 128, 1, num_heads_q=128,
+                                        topk=None if idx is None else idx.shape[2])
+    out = torch.empty((3, 1, 128, 512), dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty((3, 128, 1), dtype=torch.float32, device=DEV)
+    # first call eagerly: resolves the scratch array's device address outside the capture
+    decode_noalloc(out, lse, qd, kd, btd, ldd, md, ns, SCALE, False, fp8, idd)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode_noalloc(out, lse, qd, kd, btd, ldd, md, ns, SCALE, False, fp8, idd)
+    gen = torch.Generator(device=DEV).manual_seed(83)
+    for rep in range(3):
+        qd.copy_(torch.randn(qd.shape, generator=gen, device=DEV).to(qd.dtype))
+        if fp8:
+            kd.copy_(orc.make_fp8_cache(kc.shape[0], seed=90 + rep, lat_scale=1.0).to(DEV))
+        else:
+            kd.copy_(torch.randn(kd.shape, generator=gen, device=DEV).to(kd.dtype))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_out, ref_lse = flag_attn.flash_mla_with_kvcache(qd, kd, btd, ldd, 512, md, ns, SCALE,
+                                                            False, is_fp8_kvcache=fp8,
+                                                            indices=idd)
+        torch.cuda.synchronize()
+        _assert_same(out.cpu(), lse.cpu(), ref_out.cpu(), ref_lse.cpu())
