@@ -5,7 +5,8 @@
     python bench.py --traffic-calibrate [--workload ...]   # driver for rocprofv3 --pmc passes
 
 A step is one decode of the whole batch through the public path: scheduler metadata
-(get_mla_metadata) + decode + split combine, with every input already resident in HBM.
+(get_mla_metadata) + [sparse row translation] + decode + split combine, with every input
+already resident in HBM (the line's ``step_kernels`` lists the launches).
 The default workload is BASELINE config 2 (dense bf16, B=64, h_q=128, s_q=1, lengths
 U[4096, 8192], 64-token pages through a permuted block table).  KV pools are rotated
 between steps so consecutive steps do not hit the 256 MB last-level cache.  After the W
@@ -542,6 +543,10 @@ def main() -> None:
                     help="profiling driver: a 512 MiB device copy, then --launches decode "
                          "steps (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
     ap.add_argument("--launches", type=int, default=5)
+    ap.add_argument("--settle-launches", type=int, default=0,
+                    help="--traffic-calibrate: untimed steps after the copy and before the "
+                         "measured launches (with rocprofv3 --kernel-iteration-range, the "
+                         "counters then come from launches at the sustained clock state)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -581,11 +586,11 @@ def main() -> None:
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        for i in range(args.launches):
+        for i in range(args.settle_launches + args.launches):
             step(i)
         torch.cuda.synchronize()
-        print(f"copy_bytes={COPY_BYTES} workload={spec['name']} launches={args.launches}",
-              flush=True)
+        print(f"copy_bytes={COPY_BYTES} workload={spec['name']} "
+              f"settle_launches={args.settle_launches} launches={args.launches}", flush=True)
         return
 
     t_warm = time.perf_counter()
@@ -640,10 +645,15 @@ def main() -> None:
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(spec, q, pools[0], tables[0], lens, indices)
 
+    step_kernels = ["mla_metadata_kernel"] + (["mla_sparse_rows_kernel"] if spec["topk"] else [])
+    step_kernels += ["mla_decode_kernel", "mla_combine_kernel"]
     rec = {
         "metric": METRIC,
         "value": round(us_step, 2),
         "unit": "µs/step",
+        # what one timed step launches, in order: the scheduler metadata is recomputed every
+        # step (a model computes it once per forward pass and reuses it in every layer)
+        "step_kernels": step_kernels,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,

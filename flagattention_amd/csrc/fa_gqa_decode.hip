@@ -1,5 +1,6 @@
 // Grouped-query decode (MHA / GQA / MQA) for gfx950 over a paged or a
-// contiguous KV cache, fp16 or bf16, head dim 16..256.
+// contiguous KV cache, fp16 or bf16, head dim 16..256 (gqa_decode_kernel) and
+// 512 (gqa_decode_wide_kernel, below).
 //
 // One work-group = 4 waves = one (sequence, KV head, block of 16 query rows,
 // split).  A query row is a (query head of the group, query position) pair;
@@ -423,6 +424,267 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   }
 }
 
+// Head dim 512.  Dealing whole tiles to the waves (the kernel above) would need 32 KB of
+// V per wave and tile in LDS and 256 VGPRs of K operands per lane, so here the four waves
+// split the dims instead: wave w owns dims 128w..128w+127 and walks every 32-token tile of
+// the split.  Per tile it computes the S^T partial of its dims (K straight from global
+// memory into VGPRs, one tile ahead), the four partials are summed through LDS (one
+// barrier per tile; slots alternate by tile parity, so a wave that runs ahead never
+// overwrites a slot still being read), in the same order in every wave, so every wave
+// holds the same S^T and runs the same online softmax; then O^T += V^T P^T over its dims,
+// with its 8 KB V slice copied HBM -> LDS one tile ahead (double-buffered per wave).
+constexpr int kWideD = 512;
+constexpr int kWideDims = kWideD / 4;  // dims per wave
+
+template <typename T, bool kPaged>
+__global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
+    const fa_gqa_decode_args a) {
+  typedef typename Vec<T>::v8 T8;
+  typedef typename Vec<T>::v4 T4;
+  constexpr int D = kWideD;
+  constexpr int kRowB = 2 * kWideDims;       // 256 B: a token's slice of a wave's V tile
+  constexpr int kTileB = kGTile * kRowB;     // 8 KB per wave and tile
+  constexpr int kCopies = kTileB / 1024;     // wave-wide 16-byte copies per V slice
+  constexpr int kTokPerCopy = 1024 / kRowB;  // 4
+  constexpr int kChunks = kRowB / 16;        // 16-byte chunks of a slice row
+  constexpr int kKSteps = kWideDims / 32;    // QK k-steps per wave
+  constexpr int kDimTiles = kWideDims / 16;  // O^T dim tiles per wave
+  constexpr int kLoads = kCopies + 2 * kKSteps;
+  __shared__ __attribute__((aligned(16))) unsigned char vbuf0[4 * kTileB];
+  __shared__ __attribute__((aligned(16))) unsigned char vbuf1[4 * kTileB];
+  // S^T partials: [tile parity][wave][token half][lane]
+  __shared__ floatx4 sx[2][4][2][64];
+  __shared__ int tbl[kPaged ? kTblMax : 1];
+
+  const int split = blockIdx.x;
+  const int group = a.h_q / a.h_kv;
+  const int rows_total = group * a.m;
+  const int n_rb = cdiv(rows_total, kGRows);
+  const int hk = blockIdx.y / n_rb;
+  const int rb = blockIdx.y - hk * n_rb;
+  const int b = blockIdx.z;
+  const int wave = wave_id();
+  const int lane = threadIdx.x & 63;
+  const int G = lane >> 4, c16 = lane & 15;
+  const int dim0 = kWideDims * wave;
+
+  const int seqlen = a.seqlens ? a.seqlens[b] : a.n;
+  const int t0 = split * a.split_tokens;
+  const int t1 = min(t0 + a.split_tokens, seqlen);
+  const int ntok = max(0, t1 - t0);
+  const int ntiles = cdiv(ntok, kGTile);
+
+  const int rho = rb * kGRows + c16;
+  const bool row_ok = rho < rows_total;
+  const int jj = row_ok ? rho / a.m : 0;
+  const int mm = row_ok ? rho - jj * a.m : 0;
+  const int hq = hk * group + jj;
+  const int lim = min(a.causal ? seqlen - a.m + 1 + mm : seqlen, t1);
+
+  const float scale_log2 = a.scale * kLog2e;
+  const float ninf = -__builtin_inff();
+  const T* qp = static_cast<const T*>(a.q);
+  const unsigned char* kp = static_cast<const unsigned char*>(a.k);
+  const unsigned char* vp = static_cast<const unsigned char*>(a.v);
+
+  int blk_lo = 0;
+  bool tbl_lds = false;
+  const int bs_shift = kPaged && a.block_size > 0 && (a.block_size & (a.block_size - 1)) == 0
+                           ? __builtin_ctz(static_cast<unsigned int>(a.block_size))
+                           : -1;
+  if constexpr (kPaged) {
+    if (ntok > 0) {
+      blk_lo = t0 / a.block_size;
+      const int nblk = (t1 - 1) / a.block_size - blk_lo + 1;
+      tbl_lds = nblk <= kTblMax;
+      if (tbl_lds) {
+        for (int i = threadIdx.x; i < nblk; i += kGThreads) {
+          const int blk = blk_lo + i;
+          tbl[i] = blk < a.max_blocks_per_seq
+                       ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
+                       : -1;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Q^T operand of this wave's dims: row c16, dims dim0 + 32kk + 8G..+7
+  T8 qf[kKSteps];
+#pragma unroll
+  for (int kk = 0; kk < kKSteps; ++kk)
+    qf[kk] = row_ok ? *reinterpret_cast<const T8*>(qp + b * a.q_stride_b + hq * a.q_stride_h +
+                                                  mm * a.q_stride_m + dim0 + 32 * kk + 8 * G)
+                    : T8{};
+
+  T8 kf[2][2][kKSteps];  // [buffer][token half][k-step]
+  unsigned int kmask[2] = {0u, 0u};
+  auto issue = [&](int u, auto bt) {
+    constexpr int buf = decltype(bt)::value;
+    unsigned char* const vb = (buf == 0 ? vbuf0 : vbuf1) + wave * kTileB;
+    const int tile_start = t0 + kGTile * u;
+    const int last = t1 - 1;
+#pragma unroll
+    for (int c = 0; c < kCopies; ++c) {
+      const int r = c * kTokPerCopy + lane / kChunks;
+      const int slot = lane % kChunks;
+      const int t = min(tile_start + r, last);
+      const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t,
+                                          tbl, blk_lo, tbl_lds, bs_shift);
+      const unsigned char* src =
+          e >= 0 ? vp + 2 * (e + dim0) + 16 * (slot ^ vswz<kWideDims>(r)) : g_gqa_zero;
+      lds_dma16(src, (FA_LDS void*)(vb + c * 1024));
+    }
+    unsigned int km = 0u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = min(tile_start + 16 * h + c16, last);
+      const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t,
+                                          tbl, blk_lo, tbl_lds, bs_shift);
+      km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        const unsigned char* src = e >= 0 ? kp + 2 * (e + dim0 + 32 * kk + 8 * G) : g_gqa_zero;
+        kf[buf][h][kk] = *reinterpret_cast<const T8*>(src);
+      }
+    }
+    kmask[buf] = km;
+  };
+
+  float m_run = ninf, l_run = 0.f;
+  floatx4 acc[kDimTiles];
+#pragma unroll
+  for (int dt = 0; dt < kDimTiles; ++dt) acc[dt] = floatx4{};
+
+  auto step = [&](int u, auto bt, bool has_next) {
+    constexpr int buf = decltype(bt)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) {
+      issue(u + 1, IntTag<buf ^ 1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmem<kLoads>();  // tile u's copies and loads have landed
+    } else {
+      wait_vmem<0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int tile_start = t0 + kGTile * u;
+    // this wave's S^T partial, published for the others
+    floatx4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = floatx4{};
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk) s[h] = mfma_16x16x32(kf[buf][h][kk], qf[kk], s[h]);
+      sx[u & 1][wave][h][lane] = s[h];
+    }
+    asm volatile("" ::: "memory");
+    barrier();
+    asm volatile("" ::: "memory");
+    // the full S^T, summed in wave order (the same bits in every wave)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      floatx4 t = sx[u & 1][0][h][lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const floatx4 x = sx[u & 1][w][h][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] += x[i];
+      }
+      s[h] = t;
+    }
+    float sv[2][4];
+    float tmax = ninf;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 16 * h + 4 * G + i;
+        const bool ok = tile_start + j < lim && ((kmask[buf] >> j) & 1u);
+        sv[h][i] = ok ? s[h][i] * scale_log2 : ninf;
+        tmax = fmaxf(tmax, sv[h][i]);
+      }
+    tmax = max_xor32(max_xor16(tmax));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == ninf ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float psum = 0.f;
+    T8 pb;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(sv[h][i] - m_use);
+        psum += p;
+        pb[4 * h + i] = static_cast<T>(p);
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    const unsigned char* vb = (buf == 0 ? vbuf0 : vbuf1) + wave * kTileB;
+    const int e = c16 >> 2, qd = c16 & 3;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      const int chunk = 2 * dt + (qd >> 1);
+      const int r0 = 4 * G + e, r1 = 16 + 4 * G + e;
+      const T4 lo =
+          lds_tr4<T>(vb + r0 * kRowB + 16 * (chunk ^ vswz<kWideDims>(r0)) + 8 * (qd & 1));
+      const T4 hi =
+          lds_tr4<T>(vb + r1 * kRowB + 16 * (chunk ^ vswz<kWideDims>(r1)) + 8 * (qd & 1));
+      const T8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      floatx4 o = acc[dt];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      acc[dt] = mfma_16x16x32(va, pb, o);
+    }
+  };
+
+  if (ntiles > 0) {
+    issue(0, IntTag<0>{});
+    int u = 0;
+    for (;;) {
+      const bool n1 = u + 1 < ntiles;
+      step(u, IntTag<0>{}, n1);
+      if (!n1) break;
+      ++u;
+      const bool n2 = u + 1 < ntiles;
+      step(u, IntTag<1>{}, n2);
+      if (!n2) break;
+      ++u;
+    }
+  }
+  wait_vmem<0>();
+
+  // every wave holds the same row sums and maxima; each writes its own dims
+  const float l_col = sum_xor32(sum_xor16(l_run));
+  if (!row_ok) return;
+  const float inv = l_col > 0.f ? 1.f / l_col : 0.f;
+  const float lse = l_col > 0.f ? (m_run + log2f(l_col)) * kLn2 : ninf;
+  const int h = hk * group + jj;
+  if (a.o_part == nullptr) {
+    T* op = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h + mm * a.o_stride_m +
+            dim0 + 4 * G;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      T4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = static_cast<T>(acc[dt][i] * inv);
+      *reinterpret_cast<T4*>(op + 16 * dt) = w;
+    }
+    if (wave == 0 && G == 0 && a.lse) a.lse[(static_cast<long long>(b) * a.h_q + h) * a.m + mm] = lse;
+  } else {
+    const long long prow =
+        ((static_cast<long long>(b) * a.h_q + h) * a.m + mm) * a.num_splits + split;
+    float* op = a.o_part + prow * D + dim0 + 4 * G;
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      floatx4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = acc[dt][i] * inv;
+      *reinterpret_cast<floatx4*>(op + 16 * dt) = w;
+    }
+    if (wave == 0 && G == 0) a.lse_part[prow] = lse;
+  }
+}
+
 // LSE combine of the split partials of one query row per wave:
 // lse = logsumexp_s lse_s, out = sum_s exp(lse_s - lse) o_s.
 template <typename T>
@@ -476,8 +738,13 @@ int launch_gqa(const fa_gqa_decode_args* a, hipStream_t stream) {
     FA_GQA_CASE(128)
     FA_GQA_CASE(256)
 #undef FA_GQA_CASE
+    case kWideD:
+      hipLaunchKernelGGL((gqa_decode_wide_kernel<T, kPaged>), grid, dim3(kGThreads), 0, stream,
+                         *a);
+      break;
     default:
-      return set_error(FA_ERR_UNSUPPORTED, "head dim %d not in {16, 32, 64, 128, 256}", a->d);
+      return set_error(FA_ERR_UNSUPPORTED, "head dim %d not in {16, 32, 64, 128, 256, 512}",
+                       a->d);
   }
   FA_CHECK_HIP(hipGetLastError());
   return FA_OK;
@@ -492,8 +759,9 @@ int check_gqa(const fa_gqa_decode_args* a) {
   FA_CHECK_ARG(a->num_splits >= 1 && a->num_splits <= 65535, "num_splits %d invalid",
                a->num_splits);
   FA_CHECK_ARG(a->split_tokens >= 1, "split_tokens %d < 1", a->split_tokens);
-  FA_CHECK_ARG(a->d == 16 || a->d == 32 || a->d == 64 || a->d == 128 || a->d == 256,
-               "head dim %d not in {16, 32, 64, 128, 256}", a->d);
+  FA_CHECK_ARG(a->d == 16 || a->d == 32 || a->d == 64 || a->d == 128 || a->d == 256 ||
+                   a->d == kWideD,
+               "head dim %d not in {16, 32, 64, 128, 256, 512}", a->d);
   FA_CHECK_ARG(static_cast<long long>(a->h_kv) * cdiv((a->h_q / a->h_kv) * a->m, kGRows) <= 65535 &&
                    a->batch <= 65535,
                "grid too large: h_kv x ceil(group x m / 16) and batch must be <= 65535");

@@ -33,7 +33,7 @@ import torch
 from . import _lib
 from .errors import ArgumentError
 
-HEAD_DIMS = (16, 32, 64, 128, 256)
+HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 ROWS_PER_WG = 16
 MIN_SPLIT_TOKENS = 256
 

@@ -288,7 +288,7 @@ int64_t fa_gqa_decode_args_size(void);
 /*
  * Decode: with num_splits == 1 writes out (and lse if given); otherwise the
  * per-split partials (o_part normalised per split, lse_part) for
- * fa_gqa_combine.  Head dims 16, 32, 64, 128, 256.
+ * fa_gqa_combine.  Head dims 16, 32, 64, 128, 256, 512.
  * Replaces _paged_attn_kernel, src/flag_attn/paged.py:218-363 (paged) and
  * _fwd_split_kv_kernel, src/flag_attn/split_kv.py:28-174 (contiguous).
  */

@@ -115,11 +115,12 @@ def test_paged_attention_more_shapes(head_size, group, dtype, num_splits):
                          seed=head_size + group)
 
 
-def test_paged_attention_bad_page_is_masked():
+@pytest.mark.parametrize("d", [64, 512])
+def test_paged_attention_bad_page_is_masked(d):
     """A block-table entry outside the cache reads as a masked key instead of faulting."""
     need_gpu()
     gen = torch.Generator().manual_seed(3)
-    h, d, bs = 8, 64, 16
+    h, bs = 8, 16
     kc = torch.randn((10, h, bs, d), generator=gen).half()
     vc = torch.randn((10, h, bs, d), generator=gen).half()
     q = torch.randn((1, h, d), generator=gen).half()
@@ -274,3 +275,39 @@ def test_flash_attention_many_queries(M, N, causal):
     assert float((lse[fin] - lse_ref[fin]).abs().max()) <= 1e-3
     if causal and M > N:
         assert float(o[:, :, : M - N].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("num_seqs", [1, 8])
+@pytest.mark.parametrize("query_group_size", [1, 8])
+@pytest.mark.parametrize("block_size", [16, 128])
+@pytest.mark.parametrize("max_seq_len", [512, 2048])
+def test_paged_attention_head_size_512(num_seqs, query_group_size, block_size, max_seq_len):
+    """head_size 512, which the reference's paged_attention accepts (paged.py:45): the
+    reference sweep's inputs at that head size (the dims-split kernel)."""
+    base_paged_attention(num_seqs, 64, query_group_size, 512, block_size, max_seq_len,
+                         seed=num_seqs + query_group_size + block_size + max_seq_len)
+
+
+@pytest.mark.parametrize("num_splits,dtype,block_size", [
+    (1, torch.float16, 16), (3, torch.float16, 16), (8, torch.bfloat16, 16),
+    (0, torch.bfloat16, 24), (5, torch.float16, 8),
+])
+def test_paged_attention_head_size_512_splits(num_splits, dtype, block_size):
+    base_paged_attention(4, 16, 1 if block_size < 16 else 4, 512, block_size, 1500, num_splits,
+                         dtype=dtype, seed=num_splits + block_size)
+
+
+@pytest.mark.parametrize("M, N, causal", [(1, 3000, False), (3, 700, True)])
+def test_flash_attention_head_size_512(M, N, causal):
+    """The contiguous decode at head dim 512 (beyond the reference's flash_attention, which
+    stops at 128): split and unsplit shapes through the dims-split kernel."""
+    need_gpu()
+    for B, Hq, Hk in ((2, 4, 2), (64, 16, 4)):
+        q, k, v = _splitkv_inputs(B, Hq, Hk, M, N, 512, torch.bfloat16, "BTHD", 1.0, N + B)
+        o_ref, lse_ref = _oracle_chunked(q, k, v, causal, True)
+        o_low, _ = _oracle_chunked(q, k, v, causal, False)
+        o, lse, _, _, _ = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), causal,
+                                                    return_log_normalizer=True)
+        torch.cuda.synchronize()
+        assert_lowp_rule(o.cpu(), o_ref, o_low)
+        assert float((lse.cpu() - lse_ref).abs().max()) <= 1e-3
