@@ -162,12 +162,17 @@ __device__ inline void mfma_vacc_drain(floatx4 (&s)[2][2]) {
 // the sequence (or a page that must not be read) come back as zeros from the
 // hardware range check.  The immediate offset of an LDS-destination buffer
 // load is added to the LDS address as well, so the LDS base handed to the
-// instruction is pre-compensated by -128*G.
+// instruction is pre-compensated by -128*G.  The pages are read once per
+// launch, so the loads carry the non-temporal hint (cache policy NT): config 2
+// 121.7 -> 119.4 us and the skewed config 3 -0.8% at the same socket power
+// (the scattered sparse row gathers measured 1.5% slower with it and keep the
+// default policy).
 template <int G>
 __device__ inline void copy_block_buf(__amdgpu_buffer_rsrc_t rs, unsigned char* dst,
                                       unsigned int voff) {
+  constexpr int kNonTemporal = 2;  // CPol NT
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (FA_LDS void*)(dst + G * (kBlockBytes - 128)), 16,
-                                           voff, 0, 128 * G, 0);
+                                           voff, 0, 128 * G, kNonTemporal);
 }
 
 // fp8-e4m3 (OCP "fn") pair -> two floats, using the gfx950 converter.
