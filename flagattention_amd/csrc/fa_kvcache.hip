@@ -24,6 +24,9 @@ __device__ inline unsigned int fp8x2(float a, float b) {
 // slots through the scalar unit -- they are wave-uniform -- and their latent
 // and rope vectors, at clamped in-bounds addresses) is issued before any
 // store, so a wave waits for one memory round trip instead of one per token.
+// The new tokens are read once, with the non-temporal hint (bf16 rows 1.8%
+// faster at the prefill-sized benchmark write; the same hint on the row stores
+// measured 16% slower, so they keep the default policy).
 constexpr int kTokPerWave = 4;
 
 __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
@@ -41,9 +44,10 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
   for (int j = 0; j < kTokPerWave; ++j) {
     const int tok = min(tok0 + j, num_tokens - 1);
     slot[j] = tok0 + j < num_tokens ? slot_mapping[tok] : -1;
-    x[j] = *reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane);
+    x[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane));
     pe[j] = bf16x8{};
-    if (lane < 8) pe[j] = *reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane);
+    if (lane < 8)
+      pe[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane));
   }
 #pragma unroll
   for (int j = 0; j < kTokPerWave; ++j) {

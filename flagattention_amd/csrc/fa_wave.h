@@ -69,6 +69,17 @@ __device__ inline void lds_dma16(const void* src, FA_LDS void* lds) {
                : "memory", "m0");
 }
 
+// lds_dma16 with the non-temporal hint (nt): for streams read once per launch,
+// whose lines are better not kept in the caches (the GQA decode's K/V tiles).
+__device__ inline void lds_dma16_nt(const void* src, FA_LDS void* lds) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<__SIZE_TYPE__>(lds)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+               :
+               : "v"(src), "s"(m0)
+               : "memory", "m0");
+}
+
 // The same for 4 bytes per lane (global_load_lds_dword): lane l's word lands
 // at lds + 4 l.
 __device__ inline void lds_dma4(const void* src, FA_LDS void* lds) {
