@@ -82,25 +82,41 @@ constexpr int kTblMax = 2048;  // block-table entries of a split staged in LDS
 
 // Element offset of token `t` of sequence `b`, KV head `hk` (or -1 when the
 // token's page is outside the cache).  Paged: the page comes from the split's
-// block-table slice in LDS (tbl, first block blk_lo) when it was staged there,
-// else from the table in global memory.
-template <bool kPaged>
+// block-table slice in LDS (tbl, first block blk_lo; kTblLds) or, for a split
+// whose slice does not fit there, from the table in global memory.  The choice
+// is a template parameter, not a runtime select: with both paths in one loop
+// the compiler joins them behind a vmcnt(0) wait, which drained every tile load
+// in flight at each lookup (the D = 512 paged shape ran 0.27 of HBM).
+template <bool kPaged, bool kTblLds>
 __device__ inline long long kv_elem(const fa_gqa_decode_args& a, int b, int hk, int t,
                                     long long s0, long long sh, long long st, const int* tbl,
-                                    int blk_lo, bool tbl_lds, int bs_shift) {
+                                    int blk_lo, int bs_shift) {
   if constexpr (kPaged) {
     // power-of-two block sizes (all the usual ones) shift instead of dividing: a
     // division per load is tens of VALU instructions, ten times per tile and lane
     const int blk = bs_shift >= 0 ? t >> bs_shift : t / a.block_size;
-    const int page = tbl_lds ? tbl[blk - blk_lo]
-                     : blk < a.max_blocks_per_seq
-                         ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
-                         : -1;
+    int page;
+    if constexpr (kTblLds) {
+      page = tbl[blk - blk_lo];
+    } else {
+      page = blk < a.max_blocks_per_seq
+                 ? a.block_table[static_cast<long long>(b) * a.bt_stride_b + blk]
+                 : -1;
+    }
     if (page < 0 || page >= a.num_blocks) return -1;
     return page * s0 + hk * sh + (t - blk * a.block_size) * st;
   } else {
     return b * s0 + hk * sh + static_cast<long long>(t) * st;
   }
+}
+// The same with the table's location chosen at run time (gqa_decode_kernel, whose
+// usual paged path -- page pairs by scalar loads -- does not look pages up per lane).
+template <bool kPaged>
+__device__ inline long long kv_elem_rt(const fa_gqa_decode_args& a, int b, int hk, int t,
+                                       long long s0, long long sh, long long st, const int* tbl,
+                                       int blk_lo, bool tbl_lds, int bs_shift) {
+  return tbl_lds ? kv_elem<kPaged, true>(a, b, hk, t, s0, sh, st, tbl, blk_lo, bs_shift)
+                 : kv_elem<kPaged, false>(a, b, hk, t, s0, sh, st, tbl, blk_lo, bs_shift);
 }
 
 template <typename T, int D, bool kPaged>
@@ -263,8 +279,8 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
       const int r = c * kTokPerCopy + lane / C;
       const int slot = lane % C;
       const int t = min(tile_start + r, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t,
-                                          tbl, blk_lo, tbl_lds, bs_shift);
+      const long long e = kv_elem_rt<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h,
+                                             a.v_stride_t, tbl, blk_lo, tbl_lds, bs_shift);
       const unsigned char* src =
           e >= 0 ? vp + 2 * e + 16 * (slot ^ vswz<D>(r)) : g_gqa_zero;
       lds_dma16_nt(src, (FA_LDS void*)(vb + c * 1024));
@@ -274,8 +290,8 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int t = min(tile_start + 16 * h + c16, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t,
-                                          tbl, blk_lo, tbl_lds, bs_shift);
+      const long long e = kv_elem_rt<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h,
+                                             a.k_stride_t, tbl, blk_lo, tbl_lds, bs_shift);
       km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
@@ -454,7 +470,7 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
   constexpr int kChunks = kRowB / 16;        // 16-byte chunks of a slice row
   constexpr int kKSteps = kWideDims / 32;    // QK k-steps per wave
   constexpr int kDimTiles = kWideDims / 16;  // O^T dim tiles per wave
-  constexpr int kLoads = kCopies + 2 * kKSteps;
+  constexpr int kKLoads = 2 * kKSteps;        // K loads per wave and tile
   __shared__ __attribute__((aligned(16))) unsigned char vbuf0[4 * kTileB];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf1[4 * kTileB];
   // S^T partials: [tile parity][wave][token half][lane]
@@ -491,6 +507,16 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
   const T* qp = static_cast<const T*>(a.q);
   const unsigned char* kp = static_cast<const unsigned char*>(a.k);
   const unsigned char* vp = static_cast<const unsigned char*>(a.v);
+  // The zero row's address, taken once into scalars the compiler cannot see
+  // through, and every masked-or-not source chosen by a select that stays in
+  // front of its one load: left to itself the compiler turns the choice into
+  // two branches with a load each, joined behind a vmcnt(0) wait.
+  const unsigned char* const zero_src = [] {
+    const unsigned long long v = reinterpret_cast<unsigned long long>(g_gqa_zero);
+    unsigned int lo = static_cast<unsigned int>(v), hi = static_cast<unsigned int>(v >> 32);
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return reinterpret_cast<const unsigned char*>((static_cast<unsigned long long>(hi) << 32) | lo);
+  }();
 
   int blk_lo = 0;
   bool tbl_lds = false;
@@ -522,10 +548,16 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
                                                   mm * a.q_stride_m + dim0 + 32 * kk + 8 * G)
                     : T8{};
 
+  // Issue order per step u: K of tile u+1 at the start, V of tile u+1 after
+  // QK(u).  The compiler waits for K (VGPR loads it tracks) by counting only the
+  // K loads issued after them; a V copy issued in between (invisible to it)
+  // would then be drained too, one memory round trip per tile (the D = 512
+  // shape of the paged sweep: 993 us, 0.27 of HBM, with V issued before K).
   T8 kf[2][2][kKSteps];  // [buffer][token half][k-step]
   unsigned int kmask[2] = {0u, 0u};
-  auto issue = [&](int u, auto bt) {
+  auto issue_v = [&](int u, auto bt, auto tt) {
     constexpr int buf = decltype(bt)::value;
+    constexpr bool kTbl = decltype(tt)::value != 0;
     unsigned char* const vb = (buf == 0 ? vbuf0 : vbuf1) + wave * kTileB;
     const int tile_start = t0 + kGTile * u;
     const int last = t1 - 1;
@@ -534,22 +566,30 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
       const int r = c * kTokPerCopy + lane / kChunks;
       const int slot = lane % kChunks;
       const int t = min(tile_start + r, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.v_stride_0, a.v_stride_h, a.v_stride_t,
-                                          tbl, blk_lo, tbl_lds, bs_shift);
+      const long long e = kv_elem<kPaged, kTbl>(a, b, hk, t, a.v_stride_0, a.v_stride_h,
+                                                a.v_stride_t, tbl, blk_lo, bs_shift);
       const unsigned char* src =
-          e >= 0 ? vp + 2 * (e + dim0) + 16 * (slot ^ vswz<kWideDims>(r)) : g_gqa_zero;
+          e >= 0 ? vp + 2 * (e + dim0) + 16 * (slot ^ vswz<kWideDims>(r)) : zero_src;
+      asm volatile("" : "+v"(src));
       lds_dma16_nt(src, (FA_LDS void*)(vb + c * 1024));
     }
+  };
+  auto issue_k = [&](int u, auto bt, auto tt) {
+    constexpr int buf = decltype(bt)::value;
+    constexpr bool kTbl = decltype(tt)::value != 0;
+    const int tile_start = t0 + kGTile * u;
+    const int last = t1 - 1;
     unsigned int km = 0u;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int t = min(tile_start + 16 * h + c16, last);
-      const long long e = kv_elem<kPaged>(a, b, hk, t, a.k_stride_0, a.k_stride_h, a.k_stride_t,
-                                          tbl, blk_lo, tbl_lds, bs_shift);
+      const long long e = kv_elem<kPaged, kTbl>(a, b, hk, t, a.k_stride_0, a.k_stride_h,
+                                                a.k_stride_t, tbl, blk_lo, bs_shift);
       km |= (static_cast<unsigned int>(__ballot(e >= 0)) & 0xFFFFu) << (16 * h);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
-        const unsigned char* src = e >= 0 ? kp + 2 * (e + dim0 + 32 * kk + 8 * G) : g_gqa_zero;
+        const unsigned char* src = e >= 0 ? kp + 2 * (e + dim0 + 32 * kk + 8 * G) : zero_src;
+        asm volatile("" : "+v"(src));
         kf[buf][h][kk] = __builtin_nontemporal_load(reinterpret_cast<const T8*>(src));
       }
     }
@@ -561,13 +601,14 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
 #pragma unroll
   for (int dt = 0; dt < kDimTiles; ++dt) acc[dt] = floatx4{};
 
-  auto step = [&](int u, auto bt, bool has_next) {
+  auto step = [&](int u, auto bt, auto tt, bool has_next) {
     constexpr int buf = decltype(bt)::value;
     __builtin_amdgcn_sched_barrier(0);
     if (has_next) {
-      issue(u + 1, IntTag<buf ^ 1>{});
+      issue_k(u + 1, IntTag<buf ^ 1>{}, tt);
       __builtin_amdgcn_sched_barrier(0);
-      wait_vmem<kLoads>();  // tile u's copies and loads have landed
+      // in flight, oldest first: K(u), V(u), K(u+1): K(u) and V(u) landed
+      wait_vmem<kKLoads>();
     } else {
       wait_vmem<0>();
     }
@@ -582,6 +623,8 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
       for (int kk = 0; kk < kKSteps; ++kk) s[h] = mfma_16x16x32(kf[buf][h][kk], qf[kk], s[h]);
       sx[u & 1][wave][h][lane] = s[h];
     }
+    // V(u+1) into the other buffer, last read by PV(u-1) of this wave
+    if (has_next) issue_v(u + 1, IntTag<buf ^ 1>{}, tt);
     asm volatile("" ::: "memory");
     barrier();
     asm volatile("" ::: "memory");
@@ -642,18 +685,26 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
     }
   };
 
-  if (ntiles > 0) {
-    issue(0, IntTag<0>{});
+  auto run = [&](auto tt) {
+    issue_k(0, IntTag<0>{}, tt);
+    issue_v(0, IntTag<0>{}, tt);
     int u = 0;
     for (;;) {
       const bool n1 = u + 1 < ntiles;
-      step(u, IntTag<0>{}, n1);
+      step(u, IntTag<0>{}, tt, n1);
       if (!n1) break;
       ++u;
       const bool n2 = u + 1 < ntiles;
-      step(u, IntTag<1>{}, n2);
+      step(u, IntTag<1>{}, tt, n2);
       if (!n2) break;
       ++u;
+    }
+  };
+  if (ntiles > 0) {
+    if (!kPaged || tbl_lds) {  // uniform
+      run(IntTag<1>{});
+    } else {
+      run(IntTag<0>{});
     }
   }
   wait_vmem<0>();
