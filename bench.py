@@ -212,10 +212,41 @@ def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
     times = [run(sample) for _ in range(3)]
     t = sorted(times)[1]
     us_step = t / sample * b * 1e6
-    return {"value": round(us_step, 1), "unit": "µs/step", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{sample} of {b} sequences of {spec['name']}, median of 3, "
-                      f"scaled x{b / sample:.2f} to the full step"}
+    rec = {"value": round(us_step, 1), "unit": "µs/step", "cores": torch.get_num_threads(),
+           "kind": "port",
+           "sample": f"{sample} of {b} sequences of {spec['name']}, median of 3, "
+                     f"scaled x{b / sample:.2f} to the full step"}
+    if not spec["topk"] and not spec["causal"]:
+        rec["loop_variant"] = cpu_loop_baseline(spec, q, pool, table, lens)
+    return rec
+
+
+def cpu_loop_baseline(spec, q, pool, table, lens) -> dict:
+    """The same oracle with the gather written as the reference's testing/paged.py:37-52
+    writes it (one Python iteration per token): on one sequence of the workload, scaled to
+    the full batch, and on BASELINE config 1's shape (B=2, 16 heads, lengths 256 and 384)."""
+    from oracle import mla_oracle as orc
+
+    b = spec["batch"]
+    need = torch.unique(table[:1].flatten()).long()
+    remap = torch.full((pool.shape[0],), -1, dtype=torch.long, device=pool.device)
+    remap[need] = torch.arange(need.numel(), device=pool.device)
+    args = (q[:1].cpu(), pool[need].cpu(), remap[table[:1].long()].to(torch.int32).cpu(),
+            lens[:1].cpu(), SCALE)
+    orc.dense_decode_loop(*args)
+    t0 = time.perf_counter()
+    orc.dense_decode_loop(*args)
+    t_seq = time.perf_counter() - t0
+    c1 = orc.make_dense_inputs(2, 16, 1, [256, 384], seed=1, scale=1.0, dtype=torch.float32)
+    orc.dense_decode_loop(*c1, SCALE)
+    t0 = time.perf_counter()
+    orc.dense_decode_loop(*c1, SCALE)
+    t_c1 = time.perf_counter() - t0
+    return {"value": round(t_seq * b * 1e6, 1), "unit": "µs/step",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 of {b} sequences ({int(lens[0])} tokens), per-token loop gather, "
+                      f"scaled x{b}",
+            "config1_us": round(t_c1 * 1e6, 1)}
 
 
 # Grouped-query decode workloads (flag_attn.paged_attention / flash_attention decode), the

@@ -243,6 +243,33 @@ def dense_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.
     return out, lse
 
 
+def dense_decode_loop(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
+                      cache_seqlens: torch.Tensor, sm_scale: float,
+                      batches: Optional[Sequence[int]] = None
+                      ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``dense_decode_ref`` with the gather written as ``testing/paged.py:37-52`` writes it:
+    a Python loop over the tokens of each sequence, each row taken from page
+    ``block_table[b, j // 64]``, offset ``j % 64``, then stacked.  Same arithmetic, so the
+    same bits (``tests/test_oracle.py``); kept only as the reference-shaped CPU baseline
+    (small inputs: one Python iteration per token)."""
+    bsz, s_q, h_q, _ = q.shape
+    bl = list(range(bsz)) if batches is None else list(batches)
+    out = torch.zeros((len(bl), s_q, h_q, D_V), dtype=torch.float32)
+    lse = torch.full((len(bl), h_q, s_q), float("-inf"), dtype=torch.float32)
+    tables = block_table.tolist()
+    for i, b in enumerate(bl):
+        n = int(cache_seqlens[b])
+        rows = []
+        for j in range(n):
+            blk = int(tables[b][j // PAGE])
+            rows.append(k_cache[blk, j % PAGE, 0])
+        kv = (torch.stack(rows, dim=0) if rows else k_cache.new_zeros((0, D_QK))).float()
+        o, l = attention_lse(q[b].float().permute(1, 0, 2), kv, kv[:, :D_V], sm_scale, False)
+        out[i] = o.permute(1, 0, 2)
+        lse[i] = l
+    return out, lse
+
+
 def sparse_decode_ref(q: torch.Tensor, k_cache: torch.Tensor, block_table: torch.Tensor,
                       cache_seqlens: torch.Tensor, indices: torch.Tensor, sm_scale: float,
                       is_fp8: bool = False, batches: Optional[Sequence[int]] = None,

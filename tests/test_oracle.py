@@ -280,3 +280,18 @@ def test_fp8_tile_scales_and_write_ref():
     bf = orc.kvcache_write_ref(torch.zeros((1, 64, 1, 576), dtype=torch.bfloat16), lat, rope,
                                slots, False)
     assert torch.equal(bf.view(64, 576)[7], torch.cat([lat[4], rope[4]]))
+
+
+def test_loop_gather_equals_vectorised_bit_for_bit(golden_dir):
+    """The per-token loop restatement (the reference's testing/paged.py gather shape, used
+    only as a CPU baseline) gives the vectorised oracle's bits, and both match the float64
+    golden of the config-1 shape."""
+    q, kc, bt, lens = orc.make_dense_inputs(3, 16, 1, [256, 1, 700], seed=11, scale=1.0)
+    a_out, a_lse = orc.dense_decode_ref(q, kc, bt, lens, 192 ** -0.5)
+    b_out, b_lse = orc.dense_decode_loop(q, kc, bt, lens, 192 ** -0.5)
+    assert torch.equal(a_out, b_out) and torch.equal(a_lse, b_lse)
+    g = _load(golden_dir, "dense_cfg1.npz")
+    q, kc, bt, lens = _dense_from_golden(g)
+    out, lse = orc.dense_decode_loop(q, kc, bt, lens, float(g["sm_scale"]))
+    assert np.allclose(out.numpy(), g["out"], atol=2e-5, rtol=1e-4)
+    assert np.allclose(lse.numpy(), g["lse"], atol=2e-5)
