@@ -311,3 +311,11 @@ def test_flash_attention_head_size_512(M, N, causal):
         torch.cuda.synchronize()
         assert_lowp_rule(o.cpu(), o_ref, o_low)
         assert float((lse.cpu() - lse_ref).abs().max()) <= 1e-3
+
+
+@pytest.mark.parametrize("head_size", [64, 512])
+def test_paged_attention_split_longer_than_lds_table(head_size):
+    """A split of more than 2,048 pages (8-token pages, one split over 20,000 tokens): the
+    split's block-table slice does not fit in LDS and the pages are looked up in global
+    memory (the other loop of both kernels)."""
+    base_paged_attention(2, 4, 1, head_size, 8, 20000, 1, seed=head_size)
