@@ -9,8 +9,9 @@
 //
 // A 1024-thread work-group selects from up to 65536 keys held in registers (16-byte
 // loads, four consecutive positions per load): radix select finds the topk-th largest
-// key in four 8-bit passes over LDS histograms (each bin kept as 8 lane copies at a
-// bank-spreading stride, so lanes that hit one bin mostly update different words), and,
+// key in up to four 8-bit passes over LDS histograms (each bin kept as 8 lane copies at
+// a bank-spreading stride, so lanes that hit one bin mostly update different words;
+// the passes stop early once every key of the boundary bin is kept), and,
 // when that key is tied and only some of its copies fit, the last position to keep in
 // two more 8-bit passes over positions.  The kept positions are written in ascending
 // order: per-(block, wave) counts, one scan of those counts, lane offsets from ballots
@@ -148,10 +149,21 @@ __device__ inline void radix_select(const unsigned int (&key)[4 * NQ], int n, in
       __syncthreads();
     }
     find_bin(sm, cur, need, true, thr == 0u ? pad : 0);
-    thr = (thr << 8) | static_cast<unsigned int>(sm.info[0]);
-    need -= sm.info[1];
-    eq = sm.info[2];
+    // the bin search's results are uniform: read into scalars, so that the exit test
+    // below is a scalar compare (as a vector compare, its select of the shift came out
+    // reading a stale scalar condition code)
+    thr = (thr << 8) | static_cast<unsigned int>(__builtin_amdgcn_readfirstlane(sm.info[0]));
+    need -= __builtin_amdgcn_readfirstlane(sm.info[1]);
+    eq = __builtin_amdgcn_readfirstlane(sm.info[2]);
     cur ^= 1;
+    // every key of the boundary bin is kept: the keep set is then every key >= the
+    // bin's lowest key, with no tie to resolve -- the remaining passes are skipped
+    // (with distinct scores, usually after the third).  Not in the 64-key tiles, where
+    // the extra exits push the register allocation into spills.
+    if (NQ <= 8 && pass < 3 && need == eq) {
+      thr <<= shift;
+      break;
+    }
   }
   // Ties at thr: keep the `need` lowest slots, i.e. slots below pos_end.  The padding
   // slots (key 0) can only tie when thr == 0; they lie above every slot below n, so
