@@ -19,6 +19,7 @@
 //   part p covers global blocks [gs_p, gs_{p+1}); the segments of sequence b
 //   are the non-empty parts that intersect [G[b], G[b+1]).
 #include "fa_common.h"
+#include "fa_wave.h"
 
 namespace fa {
 namespace {
@@ -33,38 +34,46 @@ constexpr int kMaxP = FA_MLA_MAX_PARTS;
 static_assert(kMaxP <= kMetaThreadsMax && kMaxB <= 4 * kMetaThreadsMax, "one block covers a call");
 
 // Inclusive prefix sums over the work-group of a 64-bit and a 32-bit value
-// (one pair per thread): a shuffle scan inside each wave, then the wave
-// totals through LDS (two barriers; `sh64` / `sh32` are free again on return).
+// (one pair per thread): DPP scans inside each wave (no LDS round trips), then
+// the totals of the waves before this one read back from LDS (broadcast reads;
+// two barriers; `sh64` / `sh32` are free again on return).
 template <int kWaves>
 __device__ void block_incl_scan2(long long& v, int& k, long long* sh64, int* sh32) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const long long x = __shfl_up(v, off);
-    const int y = __shfl_up(k, off);
-    if (lane >= off) {
-      v += x;
-      k += y;
-    }
-  }
+  const int lane = threadIdx.x & 63, w = wave_id();
+  v = wave_incl_scan64(v);
+  k = wave_incl_scan(k);
   if (lane == 63) {
     sh64[w] = v;
     sh32[w] = k;
   }
   __syncthreads();
-  // the totals of the waves before this one: lane i < w reads wave i's, and a
-  // sum over lanes 0..15 (xor partners within the group) adds them up
-  long long bv = lane < w ? sh64[lane] : 0;
-  int bk = lane < w ? sh32[lane] : 0;
+  long long bv = 0;
+  int bk = 0;
 #pragma unroll
-  for (int off = 1; off < kWaves; off <<= 1) {
-    bv += __shfl_xor(bv, off);
-    bk += __shfl_xor(bk, off);
+  for (int i = 0; i < kWaves - 1; ++i) {
+    if (i < w) {  // uniform
+      bv += sh64[i];
+      bk += sh32[i];
+    }
   }
-  bv = __shfl(bv, 0);
-  bk = __shfl(bk, 0);
   __syncthreads();
   v += bv;
+  k += bk;
+}
+
+// block_incl_scan2 of a 32-bit value alone.
+template <int kWaves>
+__device__ void block_incl_scan(int& k, int* sh32) {
+  const int lane = threadIdx.x & 63, w = wave_id();
+  k = wave_incl_scan(k);
+  if (lane == 63) sh32[w] = k;
+  __syncthreads();
+  int bk = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves - 1; ++i) {
+    if (i < w) bk += sh32[i];  // uniform
+  }
+  __syncthreads();
   k += bk;
 }
 
@@ -174,9 +183,8 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   // 3. E[p] = number of empty parts in [0, p).
   {
     const int cnt = (t < P && gs[t] == gs[t + 1]) ? 1 : 0;
-    long long unused = 0;
     int inc = cnt;
-    block_incl_scan2<kMetaWaves>(unused, inc, sh64, sh32);
+    block_incl_scan<kMetaWaves>(inc, sh32);
     if (t < P) E[t] = inc - cnt;
     if (t == kMetaThreads - 1) E[P] = inc;
   }
@@ -210,9 +218,8 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
       segs[b - b0] = n;
       sum += n;
     }
-    long long unused = 0;
     int inc = sum;
-    block_incl_scan2<kMetaWaves>(unused, inc, sh64, sh32);
+    block_incl_scan<kMetaWaves>(inc, sh32);
     int acc = inc - sum;
     for (int b = b0; b < b1; ++b) {
       num_splits[b] = acc;

@@ -1,5 +1,5 @@
-// Wave-level helpers shared by the gfx950 decode kernels: wait counters,
-// barriers, lane ids, transposing LDS reads and cross-lane reductions.
+// Wave-level helpers shared by the gfx950 kernels: wait counters, barriers,
+// lane ids, DPP scans, transposing LDS reads and cross-lane reductions.
 #pragma once
 
 #include <utility>
@@ -37,6 +37,39 @@ template <int N>
 __device__ inline void wait_vmem() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave by DPP (no LDS round trips):
+// row shifts by 1, 2, 4, 8 within each row of 16 lanes, then lane 15 of each row
+// added to the next row (rows 1 and 3), then lane 31 to rows 2 and 3.  Lanes with
+// no source keep the `old` operand, 0.
+__device__ inline int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+// One DPP move of a 64-bit value (both halves with the same control).
+template <int kCtrl, int kRowMask>
+__device__ inline long long dpp_mov64(long long x) {
+  const unsigned int lo = static_cast<unsigned int>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xF, false));
+  const unsigned int hi = static_cast<unsigned int>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x >> 32), kCtrl, kRowMask, 0xF, false));
+  return static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo);
+}
+// wave_incl_scan for 64-bit values.
+__device__ inline long long wave_incl_scan64(long long x) {
+  x += dpp_mov64<0x111, 0xF>(x);
+  x += dpp_mov64<0x112, 0xF>(x);
+  x += dpp_mov64<0x114, 0xF>(x);
+  x += dpp_mov64<0x118, 0xF>(x);
+  x += dpp_mov64<0x142, 0xA>(x);
+  x += dpp_mov64<0x143, 0xC>(x);
+  return x;
 }
 
 // Wave index as a scalar (the compiler cannot tell that threadIdx.x / 64 is
