@@ -6,7 +6,7 @@
 //                     an all-zero tile), code = e4m3(clamp(x / scale, +-448)),
 //   bytes [528, 656)  the 64 rope dims in bf16.
 // Lane l holds latent dims 8l..8l+7 of a token; the 16 lanes of a 128-dim
-// tile reduce its amax with four lane exchanges.
+// tile (one DPP row) reduce its amax with four DPP exchanges.
 //
 // The reference has no cache writer (its tests fill caches in place); the
 // row formats are the ones fa_mla_decode_dense / fa_mla_decode_sparse read.
@@ -18,6 +18,20 @@ namespace {
 __device__ inline unsigned int fp8x2(float a, float b) {
   // two fp32 -> two OCP e4m3 codes in the low 16 bits (round to nearest even)
   return static_cast<unsigned int>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xFFFFu;
+}
+
+// Max over the 16 lanes of each DPP row (every lane gets its row's value): lane
+// exchanges xor 1, xor 2 (quad permutes), then the half-row and row mirrors.
+template <int kCtrl>
+__device__ inline float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  return v;
 }
 
 // A wave writes kTokPerWave consecutive tokens: every load (the tokens'
@@ -65,8 +79,7 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
       f[i] = static_cast<float>(x[j][i]);
       amax = fmaxf(amax, fabsf(f[i]));
     }
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = row16_max(amax);
     const float scale = amax > 0.f ? amax / 448.f : 1.f;
     uintx2 codes;
 #pragma unroll
