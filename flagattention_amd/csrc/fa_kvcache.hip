@@ -5,6 +5,10 @@
 //   bytes [512, 528)  one fp32 scale per 128 dims, scale = amax / 448 (1 for
 //                     an all-zero tile), code = e4m3(clamp(x / scale, +-448)),
 //   bytes [528, 656)  the 64 rope dims in bf16.
+// IEEE specials follow the same arithmetic: a NaN makes the tile's amax NaN,
+// hence its scale 1 (NaN > 0 fails), and NaN values stay NaN through the clamp
+// (an e4m3 NaN code); an infinity makes the scale infinite, finite values then
+// encode as zeros and infinite ones as NaN.
 // Lane l holds latent dims 8l..8l+7 of a token; the 16 lanes of a 128-dim
 // tile (one DPP row) reduce its amax with four DPP exchanges.
 //
@@ -20,17 +24,19 @@ __device__ inline unsigned int fp8x2(float a, float b) {
   return static_cast<unsigned int>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xFFFFu;
 }
 
-// Max over the 16 lanes of each DPP row (every lane gets its row's value): lane
-// exchanges xor 1, xor 2 (quad permutes), then the half-row and row mirrors.
+// Unsigned max over the 16 lanes of each DPP row (every lane gets its row's
+// value): lane exchanges xor 1, xor 2 (quad permutes), then the half-row and
+// row mirrors.
 template <int kCtrl>
-__device__ inline float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+__device__ inline unsigned int dpp_u32(unsigned int v) {
+  return static_cast<unsigned int>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
 }
-__device__ inline float row16_max(float v) {
-  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
-  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+__device__ inline unsigned int row16_max(unsigned int v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
   return v;
 }
 
@@ -72,21 +78,27 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
       if (lane < 8) *reinterpret_cast<bf16x8*>(row + 1024 + 16 * lane) = pe[j];
       continue;
     }
+    // amax over the bit patterns of |x|: for non-negative floats the unsigned
+    // order is the float order, and NaN patterns lie above +inf, so a NaN in the
+    // tile makes the amax NaN (a float max would drop it)
     float f[8];
-    float amax = 0.f;
+    unsigned int amax_bits = 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       f[i] = static_cast<float>(x[j][i]);
-      amax = fmaxf(amax, fabsf(f[i]));
+      amax_bits = max(amax_bits, __float_as_uint(f[i]) & 0x7FFFFFFFu);
     }
-    amax = row16_max(amax);
+    const float amax = __uint_as_float(row16_max(amax_bits));
     const float scale = amax > 0.f ? amax / 448.f : 1.f;
     uintx2 codes;
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(f[4 * w + i] / scale, -448.f), 448.f);
+      for (int i = 0; i < 4; ++i) {
+        const float q = f[4 * w + i] / scale;
+        v[i] = q == q ? fminf(fmaxf(q, -448.f), 448.f) : q;  // the clamp keeps NaN
+      }
       codes[w] = fp8x2(v[0], v[1]) | (fp8x2(v[2], v[3]) << 16);
     }
     *reinterpret_cast<uintx2*>(row + 8 * lane) = codes;

@@ -137,7 +137,9 @@ def fp8_tile_scales(latent: torch.Tensor) -> torch.Tensor:
     """Per-128-dim scales of the fp8 row format as the cache writer picks them:
     ``scale = amax / 448`` in fp32 over each tile of 128 latent dims (so the largest value
     maps to the largest finite e4m3 code), ``1.0`` for an all-zero tile.  ``latent``
-    ``[..., 512]`` -> scales ``[..., 4]``."""
+    ``[..., 512]`` -> scales ``[..., 4]``.  IEEE specials follow torch's arithmetic: a NaN
+    makes the tile's amax NaN and its scale ``1.0`` (``NaN > 0`` is false); an infinity
+    makes the scale infinite."""
     lat = latent.float().reshape(*latent.shape[:-1], 4, 128)
     amax = lat.abs().amax(dim=-1)
     return torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))

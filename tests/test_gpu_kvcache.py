@@ -64,6 +64,41 @@ def test_kvcache_write_bit_exact(fp8):
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+def test_kvcache_write_fp8_ieee_specials():
+    """NaN and infinities in the latent vectors: the writer follows the same arithmetic as the
+    oracle (a NaN makes its tile's amax NaN and the scale 1; an infinity makes the scale
+    infinite, finite values zeros and infinite ones NaN).  Scales and every non-NaN byte
+    are bit-exact; a NaN code may carry either sign (0x7F / 0xFF), as NaN signs are a
+    platform detail of the CPU oracle."""
+    need_gpu()
+    say("kvcache write fp8 specials")
+    nan, inf = float("nan"), float("inf")
+    lat, rope = _tokens(6, 45)
+    lat = lat.float()
+    lat[0, 3] = nan                      # tile 0: one NaN among normal values
+    lat[1, 130] = inf                    # tile 1: +inf
+    lat[1, 140] = -inf                   # (same tile) -inf
+    lat[2, 300] = -inf                   # tile 2: -inf alone
+    lat[3, 400], lat[3, 401] = nan, inf  # tile 3: NaN and +inf together
+    lat[4, :128] = nan                   # tile 0 all NaN
+    lat[4, 128:256] = 0.0                # an all-zero tile next to it
+    lat = lat.to(torch.bfloat16)
+    cache = torch.zeros((1, 64, 1, 656), dtype=torch.uint8)
+    slots = torch.arange(6, dtype=torch.int64) * 3
+    want = orc.kvcache_write_ref(cache, lat, rope, slots, True)
+    dc = cache.to(DEV)
+    flag_attn.concat_and_cache_mla(lat.to(DEV), rope.to(DEV), dc, slots.to(DEV), True)
+    torch.cuda.synchronize()
+    got = dc.cpu().view(64, 656)
+    want = want.view(64, 656)
+    assert torch.equal(got[:, 512:], want[:, 512:])  # scales and rope bytes
+    w_nan = (want[:, :512] & 0x7F) == 0x7F
+    g_nan = (got[:, :512] & 0x7F) == 0x7F
+    assert torch.equal(w_nan, g_nan)
+    assert int(w_nan.sum()) >= 128 + 4  # the NaN inputs and inf / inf
+    assert torch.equal(got[:, :512][~w_nan], want[:, :512][~w_nan])
+
+
 def test_kvcache_write_int32_slots_and_strided_inputs():
     need_gpu()
     lat, rope = _tokens(64, 40)
