@@ -448,12 +448,16 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
 // Head dim 512.  Dealing whole tiles to the waves (the kernel above) would need 32 KB of
 // V per wave and tile in LDS and 256 VGPRs of K operands per lane, so here the four waves
 // split the dims instead: wave w owns dims 128w..128w+127 and walks every 32-token tile of
-// the split.  Per tile it computes the S^T partial of its dims (K straight from global
-// memory into VGPRs, one tile ahead), the four partials are summed through LDS (one
-// barrier per tile; slots alternate by tile parity, so a wave that runs ahead never
-// overwrites a slot still being read), in the same order in every wave, so every wave
-// holds the same S^T and runs the same online softmax; then O^T += V^T P^T over its dims,
-// with its 8 KB V slice copied HBM -> LDS one tile ahead (double-buffered per wave).
+// the split.  Per tile it computes the S^T partial of its dims, the four partials are
+// summed through LDS (one barrier per tile; slots alternate by tile parity, so a wave
+// that runs ahead never overwrites a slot still being read), in the same order in every
+// wave, so every wave holds the same S^T and runs the same online softmax; then O^T +=
+// V^T P^T over its dims.  The wave's 8 KB K and V slices of a tile are both copied
+// HBM -> LDS (double-buffered per wave), requested together at the start of the step
+// before their tile's, so each has a whole step to land.  (With K loaded into VGPRs
+// instead, the compiler's wait for K counts only K loads and would also drain V copies
+// issued after them, which kept V requested only half a step ahead: 426 us at the
+// benchmark shape, B = 64, 32 heads, context 4,096.)
 constexpr int kWideD = 512;
 constexpr int kWideDims = kWideD / 4;  // dims per wave
 
@@ -470,7 +474,10 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
   constexpr int kChunks = kRowB / 16;        // 16-byte chunks of a slice row
   constexpr int kKSteps = kWideDims / 32;    // QK k-steps per wave
   constexpr int kDimTiles = kWideDims / 16;  // O^T dim tiles per wave
-  constexpr int kKLoads = 2 * kKSteps;        // K loads per wave and tile
+  constexpr int kKLoads = 2 * kKSteps;        // K copies per wave and tile
+  static_assert(kKLoads * 1024 == kTileB && kCopies == kKLoads, "a K slice = a V slice = 8 KB");
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf0[4 * kTileB];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf1[4 * kTileB];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf0[4 * kTileB];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf1[4 * kTileB];
   // S^T partials: [tile parity][wave][token half][lane]
@@ -548,12 +555,12 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
                                                   mm * a.q_stride_m + dim0 + 32 * kk + 8 * G)
                     : T8{};
 
-  // Issue order per step u: K of tile u+1 at the start, V of tile u+1 after
-  // QK(u).  The compiler waits for K (VGPR loads it tracks) by counting only the
-  // K loads issued after them; a V copy issued in between (invisible to it)
-  // would then be drained too, one memory round trip per tile (the D = 512
-  // shape of the paged sweep: 993 us, 0.27 of HBM, with V issued before K).
-  T8 kf[2][2][kKSteps];  // [buffer][token half][k-step]
+  // Step u requests K and V of tile u+1 at its start and waits for those of
+  // tile u (16 copies per wave and tile, counted in vmcnt; the loop issues no
+  // other vector memory operation).  K slice layout: copy c = (token half h,
+  // k-step kk) = 4h + kk holds, at 16 l, lane l's operand: token 16h + l % 16,
+  // dims dim0 + 32kk + 8 (l / 16)..+7, so the QK reads are 16 consecutive bytes
+  // per lane.
   unsigned int kmask[2] = {0u, 0u};
   auto issue_v = [&](int u, auto bt, auto tt) {
     constexpr int buf = decltype(bt)::value;
@@ -577,6 +584,7 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
   auto issue_k = [&](int u, auto bt, auto tt) {
     constexpr int buf = decltype(bt)::value;
     constexpr bool kTbl = decltype(tt)::value != 0;
+    unsigned char* const kb = (buf == 0 ? kbuf0 : kbuf1) + wave * kTileB;
     const int tile_start = t0 + kGTile * u;
     const int last = t1 - 1;
     unsigned int km = 0u;
@@ -590,7 +598,7 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
       for (int kk = 0; kk < kKSteps; ++kk) {
         const unsigned char* src = e >= 0 ? kp + 2 * (e + dim0 + 32 * kk + 8 * G) : zero_src;
         asm volatile("" : "+v"(src));
-        kf[buf][h][kk] = __builtin_nontemporal_load(reinterpret_cast<const T8*>(src));
+        lds_dma16_nt(src, (FA_LDS void*)(kb + (kKSteps * h + kk) * 1024));
       }
     }
     kmask[buf] = km;
@@ -605,26 +613,32 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
     constexpr int buf = decltype(bt)::value;
     __builtin_amdgcn_sched_barrier(0);
     if (has_next) {
+      // K(u+1) and V(u+1) into the other buffers, last read by QK(u-1) / PV(u-1)
+      // of this wave
       issue_k(u + 1, IntTag<buf ^ 1>{}, tt);
+      issue_v(u + 1, IntTag<buf ^ 1>{}, tt);
       __builtin_amdgcn_sched_barrier(0);
-      // in flight, oldest first: K(u), V(u), K(u+1): K(u) and V(u) landed
-      wait_vmem<kKLoads>();
+      // in flight, oldest first: K(u), V(u), K(u+1), V(u+1): K(u) and V(u) landed
+      wait_vmem<kKLoads + kCopies>();
     } else {
       wait_vmem<0>();
     }
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     const int tile_start = t0 + kGTile * u;
+    const unsigned char* const kb = (buf == 0 ? kbuf0 : kbuf1) + wave * kTileB;
     // this wave's S^T partial, published for the others
     floatx4 s[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       s[h] = floatx4{};
 #pragma unroll
-      for (int kk = 0; kk < kKSteps; ++kk) s[h] = mfma_16x16x32(kf[buf][h][kk], qf[kk], s[h]);
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        const T8 kv = *reinterpret_cast<const T8*>(kb + (kKSteps * h + kk) * 1024 + 16 * lane);
+        s[h] = mfma_16x16x32(kv, qf[kk], s[h]);
+      }
       sx[u & 1][wave][h][lane] = s[h];
     }
-    // V(u+1) into the other buffer, last read by PV(u-1) of this wave
-    if (has_next) issue_v(u + 1, IntTag<buf ^ 1>{}, tt);
     asm volatile("" ::: "memory");
     barrier();
     asm volatile("" ::: "memory");
