@@ -65,9 +65,12 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
     const int tok = min(tok0 + j, num_tokens - 1);
     slot[j] = tok0 + j < num_tokens ? slot_mapping[tok] : -1;
     x[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kv_c + tok * kv_c_stride + 8 * lane));
+    // rope chunk c (16 bytes) in lane c + 1: lane 0 carries the fp8 row's scales,
+    // which sit just before the rope bytes, so both leave in one store
     pe[j] = bf16x8{};
-    if (lane < 8)
-      pe[j] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * lane));
+    if (lane >= 1 && lane <= 8)
+      pe[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const bf16x8*>(k_pe + tok * k_pe_stride + 8 * (lane - 1)));
   }
 #pragma unroll
   for (int j = 0; j < kTokPerWave; ++j) {
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
     unsigned char* row = cache + (slot[j] >> 6) * block_stride + (slot[j] & 63) * row_stride;
     if (!fp8) {
       *reinterpret_cast<bf16x8*>(row + 16 * lane) = x[j];
-      if (lane < 8) *reinterpret_cast<bf16x8*>(row + 1024 + 16 * lane) = pe[j];
+      if (lane >= 1 && lane <= 8) *reinterpret_cast<bf16x8*>(row + 1008 + 16 * lane) = pe[j];
       continue;
     }
     // amax over the bit patterns of |x|: for non-negative floats the unsigned
@@ -88,22 +91,54 @@ __global__ __launch_bounds__(256) void mla_kvcache_write_kernel(
       f[i] = static_cast<float>(x[j][i]);
       amax_bits = max(amax_bits, __float_as_uint(f[i]) & 0x7FFFFFFFu);
     }
-    const float amax = __uint_as_float(row16_max(amax_bits));
+    const unsigned int amax_row = row16_max(amax_bits);
+    const float amax = __uint_as_float(amax_row);
     const float scale = amax > 0.f ? amax / 448.f : 1.f;
+    // x / scale, bit-identical to the IEEE division: with y = 1 / scale (one
+    // IEEE division per token), q = x * y is corrected once by its exact
+    // residual r = x - scale * q (Markstein's FMA correction, q' = q + r * y).
+    // The writer's divisors are scale = amax / 448 for bf16 amax, so every
+    // (x, scale) pair is one of 128 x 128 mantissa pairs times a power of two,
+    // and all 16,384 give the IEEE quotient (checked exhaustively with exact
+    // arithmetic by the CPU tests); powers of two scale every step exactly.  The
+    // sign is taken from x so that -0 stays -0.  Tiles with a NaN or an
+    // infinity (a non-finite amax; the residual of an infinite x is NaN) and
+    // scales below 2^-60 (all-tiny tiles: the residual of a quotient that can
+    // still round to a non-zero code could underflow) divide instead.
+    const bool fast_div = amax_row < 0x7F800000u && scale >= 0x1p-60f;
+    const float y = 1.f / scale;
     uintx2 codes;
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float q = f[4 * w + i] / scale;
+        const float x = f[4 * w + i];
+        float q;
+        if (fast_div) {
+          const float q0 = x * y;
+          const float r = __builtin_fmaf(-scale, q0, x);
+          q = __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+        } else {
+          q = x / scale;
+        }
         v[i] = q == q ? fminf(fmaxf(q, -448.f), 448.f) : q;  // the clamp keeps NaN
       }
       codes[w] = fp8x2(v[0], v[1]) | (fp8x2(v[2], v[3]) << 16);
     }
     *reinterpret_cast<uintx2*>(row + 8 * lane) = codes;
-    if ((lane & 15) == 0) *reinterpret_cast<float*>(row + 512 + 4 * (lane >> 4)) = scale;
-    if (lane < 8) *reinterpret_cast<bf16x8*>(row + 528 + 16 * lane) = pe[j];
+    // bytes 512..655: the four tile scales (lanes 0, 16, 32, 48 hold them) from
+    // lane 0, then the rope chunks from lanes 1..8 -- one store instruction
+    const int sb = __float_as_int(scale);
+    uintx4 tail;
+    tail[0] = static_cast<unsigned int>(__builtin_amdgcn_readlane(sb, 0));
+    tail[1] = static_cast<unsigned int>(__builtin_amdgcn_readlane(sb, 16));
+    tail[2] = static_cast<unsigned int>(__builtin_amdgcn_readlane(sb, 32));
+    tail[3] = static_cast<unsigned int>(__builtin_amdgcn_readlane(sb, 48));
+    if (lane <= 8) {
+      const uintx4 v = lane == 0 ? tail : __builtin_bit_cast(uintx4, pe[j]);
+      *reinterpret_cast<uintx4*>(row + 512 + 16 * lane) = v;
+    }
   }
 }
 
