@@ -448,8 +448,23 @@ __global__ __launch_bounds__(kTkThreads) void topk_merge_kernel(
     for (int i = tid; i < topk; i += kTkThreads) o[i] = i < n_row ? i : -1;
     return;
   }
-  // list slot v -> chunk c with pre[c] <= v < pre[c + 1], element v - pre[c] of its list
+  // list slot v -> chunk c with pre[c] <= v < pre[c + 1], element v - pre[c] of its list.
+  // When every list is full (kl entries: every chunk longer than kl), the row's lists
+  // are one block and slot v is its entry v: the keys are loaded from there beside the
+  // counts, instead of after them, and loaded again through the counts only for a row
+  // with a short list.
   const long long lbase = static_cast<long long>(row) * nchunks;
+  const int nfull = nchunks * kl;
+  unsigned int key[4 * NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int v0 = 4 * (q * kTkThreads + tid);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int v = v0 + c;
+      key[4 * q + c] = cand_key[lbase * kl + (v < nfull ? v : nfull - 1)];
+    }
+  }
   int pre[kTkMaxChunks + 1];
   pre[0] = 0;
 #pragma unroll
@@ -466,14 +481,14 @@ __global__ __launch_bounds__(kTkThreads) void topk_merge_kernel(
   };
   tk_begin(sm);
   __syncthreads();
-  unsigned int key[4 * NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int v0 = 4 * (q * kTkThreads + tid);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int v = v0 + c;
-      key[4 * q + c] = v < n ? cand_key[where(v)] : 0u;
+      if (n != nfull) key[4 * q + c] = cand_key[where(v < n ? v : n - 1)];  // uniform
+      key[4 * q + c] = v < n ? key[4 * q + c] : 0u;  // slots past the list: padding
     }
   }
 #pragma unroll
