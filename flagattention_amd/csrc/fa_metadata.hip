@@ -77,21 +77,34 @@ __device__ void block_incl_scan(int& k, int* sh32) {
   k += bk;
 }
 
-// Largest i in [0, n) with a[i] <= x (a non-decreasing, a[0] <= x).
+// Largest i in [0, n) with a[i] <= x (a non-decreasing, a[0] <= x).  An 8-way search:
+// the answer lies in [lo, hi) with a[lo] <= x; each round probes lo + k * step for
+// k = 1..7 (seven independent LDS reads, one latency per round instead of one per
+// halving), and the probes that pass form a prefix.  n <= 64 takes two rounds.
 __device__ int last_le(const long long* a, int n, long long x) {
-  int lo = 0, hi = n - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (a[mid] <= x) lo = mid; else hi = mid - 1;
+  int lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int step = (hi - lo + 7) >> 3;
+    int cnt = 0;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) {
+      const int p = lo + k * step;
+      const long long v = a[p < hi ? p : hi - 1];
+      cnt += (p < hi && v <= x) ? 1 : 0;
+    }
+    lo += cnt * step;
+    hi = min(hi, lo + step);
   }
   return lo;
 }
 
-// floor(a / b) for 0 <= a < 2^53, b > 0: a double-precision estimate, made
-// exact by integer correction (a stays below 2^48 here: P * W with P <= 2^10
-// and W <= 4096 * (2^25 + 4)).
-__device__ inline long long floor_div(long long a, long long b) {
-  long long q = static_cast<long long>(static_cast<double>(a) / static_cast<double>(b));
+// floor(a / b) for 0 <= a < 2^48, b > 0, given rb = 1.0 / b: the double-precision
+// estimate a * rb is within 2^48 * 2^-52 of a / b, so one integer correction step
+// makes it exact (a stays below 2^48 here: P * W with P <= 2^10 and W <= 4096 *
+// (2^25 + 4)).  The divisors P and W are the same for every part, so each thread
+// divides once per divisor and multiplies per quotient.
+__device__ inline long long floor_div(long long a, long long b, double rb) {
+  long long q = static_cast<long long>(static_cast<double>(a) * rb);
   while (q * b > a) --q;
   while ((q + 1) * b <= a) ++q;
   return q;
@@ -120,6 +133,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
 
   const int t = threadIdx.x;
   const int ipt = cdiv(B, kMetaThreads);  // sequences per thread (<= 4)
+  const double rP = 1.0 / static_cast<double>(P);
   const int b0 = min(B, t * ipt), b1 = min(B, b0 + ipt);
 
   // 1. G and the count K of non-empty sequences, scanned together; then
@@ -152,13 +166,16 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   __syncthreads();
   const long long W = C[B];
   const long long NB = G[B];
+  const double rW = 1.0 / static_cast<double>(W > 0 ? W : 1);
 
   // 2. part starts x_p = ceil(p W / P) on the cost line -> global blocks; and
   //    per sequence, the parts that hold its first and last block, in closed
   //    form: gs_p <= G[b] exactly when x_p <= C[b] + overhead, and
   //    gs_p < G[b+1] exactly when x_p < C[b+1], and x_p grows with p.
   for (int p = t; p <= P; p += kMetaThreads) {
-    const long long x = floor_div(static_cast<long long>(p) * W + P - 1, P);
+    // x_P = W exactly: no division for the last cut (with P = threads it is the one
+    // part a thread would otherwise take second)
+    const long long x = p == P ? W : floor_div(static_cast<long long>(p) * W + P - 1, P, rP);
     long long v;
     int own;
     if (x >= W) {
@@ -174,8 +191,8 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   }
   for (int b = b0; b < b1; ++b) {
     if (G[b + 1] > G[b]) {
-      pf[b] = static_cast<int>(floor_div((C[b] + overhead) * P, W));
-      pl[b] = static_cast<int>(floor_div((C[b + 1] - 1) * P, W));
+      pf[b] = static_cast<int>(floor_div((C[b] + overhead) * P, W, rW));
+      pl[b] = static_cast<int>(floor_div((C[b + 1] - 1) * P, W, rW));
     }
   }
   __syncthreads();
