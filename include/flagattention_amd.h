@@ -178,7 +178,9 @@ int fa_mla_combine(const fa_mla_decode_args* args, void* stream);
  * unspecified which).  fp8 == 0: the 1152-byte bf16 row latent | rope.
  * fp8 != 0: the 656-byte row of fa_mla_decode_sparse(fp8): 512 e4m3 codes,
  * one fp32 scale per 128 dims (scale = amax / 448, 1 for an all-zero tile,
- * code = e4m3(clamp(x / scale, +-448)), round to nearest even), 64 bf16 rope.
+ * code = e4m3(clamp(x / scale, +-448)), round to nearest even, x / scale as
+ * the IEEE fp32 quotient), 64 bf16 rope.  A NaN in a tile makes its scale 1
+ * and stays NaN (an e4m3 NaN code); an infinity makes the scale infinite.
  * Strides: kv_c_stride / k_pe_stride in elements, cache strides in bytes.
  * No counterpart in the reference (it has no cache writer); this is the
  * producer of the row layouts the MLA decode reads.
