@@ -1,7 +1,8 @@
 """MLA decode benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload dense|skew|sparse|sparse_fp8]
-    python bench.py --workload gqa_paged|gqa_splitkv|topk       # the other decode-path kernels
+    python bench.py --workload gqa_paged|gqa_splitkv|gqa_paged_d512|topk|kvcache|kvcache_fp8
+                                                           # the other decode-path kernels
     python bench.py --traffic-calibrate [--workload ...]   # driver for rocprofv3 --pmc passes
 
 A step is one decode of the whole batch through the public path: scheduler metadata
@@ -258,6 +259,9 @@ GQA_WORKLOADS = {
                       group=8, d=128, block=16, ctx=8192, seed=11),
     "gqa_splitkv": dict(name="gqa_splitkv_b2_h16_d128_ctx262144", kind="splitkv", batch=2,
                         h_q=16, group=1, d=128, ctx=262144, seed=12),
+    # head size 512 (the reference's largest paged_attention head size)
+    "gqa_paged_d512": dict(name="gqa_paged_b64_h32_g8_d512_ctx4096", kind="paged", batch=64,
+                           h_q=32, group=8, d=512, block=16, ctx=4096, seed=16),
 }
 GQA_METRIC = "GQA decode µs/step + achieved HBM GB/s (% of roofline)"
 
@@ -345,7 +349,7 @@ def run_gqa(args) -> None:
                    "ctx": ctx, "block_size": spec.get("block")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "gqa_decode_kernel", "kernel_launches_timed": len(dec),
+                     "kernel": "gqa_decode_wide_kernel" if d == 512 else "gqa_decode_kernel", "kernel_launches_timed": len(dec),
                      "kernel_us_mean": round(dec_us, 2), "bytes_per_launch": nbytes,
                      "flops_per_launch": flops,
                      "tflops": round(flops / (dec_us * 1e-6) / 1e12, 2)},
