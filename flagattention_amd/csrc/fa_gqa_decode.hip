@@ -309,16 +309,16 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
   for (int dt = 0; dt < kDimTiles; ++dt) acc[dt] = floatx4{};
 
   // tiles wave, wave + 4, ...: processed in pairs so the buffer index is a constant
+  // Tile u+4 (this wave's next) is requested after QK(u), not before: the compiler
+  // waits for the K registers by counting only the K loads issued after them, so a
+  // later tile's copies and loads issued ahead of QK(u) were drained with tile u --
+  // one memory round trip per step (its waits came out vmcnt(4)..vmcnt(0) at QK).
+  // Requested here, tile u+4 has the rest of this step and the other waves' steps to
+  // land.
   auto step = [&](int u, auto bt, bool has_next) {
     constexpr int buf = decltype(bt)::value;
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next) {
-      issue(u + 4, IntTag<buf ^ 1>{});
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmem<kLoads>();  // tile u's copies and loads have landed
-    } else {
-      wait_vmem<0>();
-    }
+    wait_vmem<0>();  // tile u's copies and loads (requested one step ago) have landed
     __builtin_amdgcn_sched_barrier(0);
     const int tile_start = t0 + kGTile * u;
     floatx4 s[2];
@@ -328,6 +328,9 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) s[h] = mfma_16x16x32(kf[buf][h][kk], qf[kk], s[h]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) issue(u + 4, IntTag<buf ^ 1>{});
+    __builtin_amdgcn_sched_barrier(0);
     // softmax down the column: tokens tile_start + 16h + 4G + i
     float sv[2][4];
     float tmax = ninf;
