@@ -158,35 +158,68 @@ def algorithmic_work(spec, lens_cpu, indices) -> tuple:
     return nbytes, flops
 
 
-# The sources the MLA decode kernel is compiled from (its translation unit and the
-# headers it includes); a traffic record holds only while these are unchanged.
-DECODE_SOURCES = ("flagattention_amd/csrc/fa_decode.hip", "flagattention_amd/csrc/fa_common.h",
-                  "flagattention_amd/csrc/fa_wave.h", "include/flagattention_amd.h")
+# The sources each timed kernel is compiled from (its translation unit and the headers
+# it includes); a traffic record holds only while these are unchanged.
+_SHARED = ("flagattention_amd/csrc/fa_common.h", "flagattention_amd/csrc/fa_wave.h",
+           "include/flagattention_amd.h")
+DECODE_SOURCES = ("flagattention_amd/csrc/fa_decode.hip",) + _SHARED
+KERNEL_SOURCES = {
+    "mla_decode": DECODE_SOURCES,
+    "gqa_decode": ("flagattention_amd/csrc/fa_gqa_decode.hip",) + _SHARED,
+    "topk": ("flagattention_amd/csrc/fa_topk.hip",) + _SHARED,
+    "kvcache": ("flagattention_amd/csrc/fa_kvcache.hip",) + _SHARED,
+}
 
 
-def kernel_sources_sha() -> str:
-    """sha256 (16 hex) over the decode kernel's sources, as recorded in profiles/."""
+def kernel_sources_sha(family: str = "mla_decode") -> str:
+    """sha256 (16 hex) over a kernel family's sources, as recorded in profiles/."""
     import hashlib
     h = hashlib.sha256()
-    for rel in DECODE_SOURCES:
+    for rel in KERNEL_SOURCES[family]:
         h.update(rel.encode())
         with open(os.path.join(ROOT, rel), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
 
 
-def recorded_traffic(workload_name: str):
-    """HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE
-    (copy-calibrated, profiles/traffic.json) -- only if recorded for these exact kernel
-    sources; otherwise None."""
+def recorded_traffic(workload_name: str, family: str = "mla_decode"):
+    """HBM bytes per launch of the timed kernel(s) measured with rocprofv3 FETCH_SIZE +
+    WRITE_SIZE (copy-calibrated, profiles/traffic.json) -- only if recorded for these exact
+    kernel sources; otherwise None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
         rec = json.load(fh).get(workload_name)
-    if not rec or rec.get("csrc_sha") != kernel_sources_sha():
+    if not rec or rec.get("csrc_sha") != kernel_sources_sha(family):
         return None
     return int(rec["hbm_read_bytes"]) + int(rec["hbm_write_bytes"])
+
+
+TRAFFIC_SOURCE = "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)"
+
+
+def with_traffic_source(rec: dict) -> dict:
+    """Names where a measured `traffic` comes from."""
+    if rec["roofline"].get("traffic") is not None:
+        rec["roofline"]["traffic_source"] = TRAFFIC_SOURCE
+    return rec
+
+
+def calibrate_then(step, args, name: str) -> None:
+    """--traffic-calibrate: the 512 MiB device copy whose counter values scale the kernel's,
+    then --settle-launches + --launches steps (the profiler's counter passes)."""
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for i in range(args.settle_launches + args.launches):
+        step(i)
+    torch.cuda.synchronize()
+    print(f"copy_bytes={COPY_BYTES} workload={name} settle_launches={args.settle_launches} "
+          f"launches={args.launches}", flush=True)
 
 
 def cpu_baseline(spec, q, pool, table, lens, indices) -> dict:
@@ -319,6 +352,9 @@ def run_gqa(args) -> dict:
         q, k, v = c
         return flag_attn.flash_attention(q, k, v, False)
 
+    if args.traffic_calibrate:
+        calibrate_then(step, args, spec["name"])
+        return None
     t_warm = time.perf_counter()
     for i in range(args.warmup):
         step(i)
@@ -357,14 +393,15 @@ def run_gqa(args) -> dict:
         "config": {"workload": spec["name"], "batch": b, "h_q": h_q, "h_kv": h_kv, "d": d,
                    "ctx": ctx, "block_size": spec.get("block")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": recorded_traffic(spec["name"], "gqa_decode"),
                      "kernel": "gqa_decode_wide_kernel" if d == 512 else "gqa_decode_kernel", "kernel_launches_timed": len(dec),
                      "kernel_us_mean": round(dec_us, 2), "bytes_per_launch": nbytes,
                      "flops_per_launch": flops,
                      "tflops": round(flops / (dec_us * 1e-6) / 1e12, 2)},
         "cpu_baseline": cpu,
     }
-    return rec
+    return with_traffic_source(rec)
 
 
 def gqa_cpu_baseline(spec, inputs, scale) -> dict:
@@ -423,6 +460,9 @@ def run_topk(args) -> dict:
     def step(i):
         return flag_attn.topk_indices(scores[i % 2], lens, topk, out=out)
 
+    if args.traffic_calibrate:
+        calibrate_then(step, args, spec["name"])
+        return None
     t_warm = time.perf_counter()
     for i in range(args.warmup):
         step(i)
@@ -474,12 +514,15 @@ def run_topk(args) -> dict:
         "config": {"workload": spec["name"], "batch": b, "s_q": s_q, "length": length,
                    "topk": topk},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "topk_indices_kernel", "kernel_launches_timed": len(dec),
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": recorded_traffic(spec["name"], "topk"),
+                     # one topk_indices call: the chunk and merge kernels of the two-stage plan
+                     "kernel": "topk_chunk_kernel+topk_merge_kernel",
+                     "kernel_launches_timed": len(dec),
                      "kernel_us_mean": round(k_us, 2), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }
-    return rec
+    return with_traffic_source(rec)
 
 
 KVC_WORKLOADS = {
@@ -513,6 +556,9 @@ def run_kvcache(args) -> dict:
     def step(i):
         flag_attn.concat_and_cache_mla(lat[i % 2], rope[i % 2], cache, slots, fp8)
 
+    if args.traffic_calibrate:
+        calibrate_then(step, args, spec["name"])
+        return None
     t_warm = time.perf_counter()
     for i in range(args.warmup):
         step(i)
@@ -565,12 +611,13 @@ def run_kvcache(args) -> dict:
         "config": {"workload": spec["name"], "tokens": t, "pages": pages,
                    "row_bytes": 656 if fp8 else 1152},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": recorded_traffic(spec["name"], "kvcache"),
                      "kernel": "mla_kvcache_write_kernel", "kernel_launches_timed": len(dec),
                      "kernel_us_mean": round(k_us, 2), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }
-    return rec
+    return with_traffic_source(rec)
 
 
 def main() -> None:
@@ -666,16 +713,7 @@ def run_mla(args) -> dict | None:
 
     if args.traffic_calibrate:
         # the copy's counter value over its known byte count scales the decode's values
-        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        for i in range(args.settle_launches + args.launches):
-            step(i)
-        torch.cuda.synchronize()
-        print(f"copy_bytes={COPY_BYTES} workload={spec['name']} "
-              f"settle_launches={args.settle_launches} launches={args.launches}", flush=True)
+        calibrate_then(step, args, spec["name"])
         return None
 
     t_warm = time.perf_counter()
@@ -718,7 +756,7 @@ def run_mla(args) -> dict | None:
         roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(mfma_frac, 4), "traffic": traffic}
     if traffic is not None:
-        roof["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)"
+        roof["traffic_source"] = TRAFFIC_SOURCE
     roof.update({"kernel": "mla_decode_kernel", "kernel_launches_timed": len(dec_ms),
                  "kernel_us_mean": round(dec_us_mean, 2),
                  "kernel_us_median": round(dec_us_med, 2), "bytes_per_launch": nbytes,
