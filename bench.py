@@ -16,7 +16,7 @@ steps have run since the start of the warm-up (reported as ``settle_s``): with o
 warm-up steps the GPU has not reached its steady clocks and the decode kernel runs ~20%
 slower.
 
-With no --workload (the driver's invocation) the line also carries `other_workloads`: every
+With no --workload (the default invocation) the line also carries `other_workloads`: every
 other workload above, measured briefly in the same process after the flagship (OTHER_STEPS
 timed steps each, no CPU baseline) -- its µs/step, its kernel's mean time by events and
 roofline fraction -- so that one default run records every workload; --no-extras skips it.
