@@ -193,3 +193,19 @@ def test_two_stage_large_topk(length, topk, kind):
     else:
         scores = torch.randint(-4, 4, (2, 2, length), generator=gen).float()
     _run(scores, [length, length - 3000], topk, causal=True)
+
+
+@pytest.mark.parametrize("high", [[2], [0, 3], [1, 2, 3]])
+@pytest.mark.parametrize("kind", ["shift", "const"])
+def test_two_stage_concentrated_chunks(high, kind):
+    """Whole chunks (16384 scores) of large scores -- shifted normal ones, or one constant:
+    the row's top-k then lies in one to three chunks (with the constant, as the lowest
+    positions of the first such chunk), and the other chunks' candidates all lose."""
+    gen = torch.Generator().manual_seed(sum(high))
+    scores = torch.randn((2, 1, 65536), generator=gen)
+    for c in high:
+        if kind == "shift":
+            scores[:, 0, c * 16384:(c + 1) * 16384] += 50.0
+        else:
+            scores[:, 0, c * 16384:(c + 1) * 16384] = 50.0
+    _run(scores, [65536, 60000], 2048, causal=False)
