@@ -454,9 +454,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
     // to 4) sit in this wave's LDS slot, read at the start of each QK with
     // the first K operands, and go there directly (LDS-destination loads, 16
     // bytes per lane = the slot's lane layout).  The AGPRs hold the O
-    // accumulators.  Issued behind the first two tile requests, so that a
-    // wait for Q does not hold those back.  Rows past the last one read the
-    // zero row.
+    // accumulators.  Dense: requested between the first tiles' page id and
+    // their copies, so that step 0 waits for Q and tile 0 but not for tile 1
+    // (vmcnt counts in order; behind both tiles' copies, the first wait for Q
+    // also waited for tile 1: config 2 0.75% slower).  Sparse: beside the rows
+    // of tiles 0 and 1 (the prologue).  Rows past the last one read the zero
+    // row.
     constexpr int kQInLds = kMode == kDense ? 0 : kQLds;
     bf16x8 qf[kQOps - kQInLds];
     auto load_q = [&]() {
@@ -650,12 +653,14 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
     };
 
-    // ---- prologue: tiles 0 and 1 requested (dense: before Q, in the first pass;
-    // sparse: Q is requested beside the rows of tiles 0 and 1, so that its
-    // latency overlaps the wait for those rows, which the tile copies need) ----
+    // ---- prologue: tiles 0 and 1 requested, Q with them in the first pass
+    // (dense: after the tiles' page id, before their copies; sparse: beside the
+    // rows of tiles 0 and 1, so that its latency overlaps the wait for those
+    // rows, which the tile copies need) ----
     auto prologue = [&](bool with_q) {
       if constexpr (kMode == kDense) {
         const int p0 = load_page(0);  // tiles 0 and 1 share a page
+        if (with_q) load_q();  // uniform
         copy_all(dense_req(0, page_of(0, p0), kv_buf0, &vq[0]));
         copy_all(dense_req(1, page_of(1, p0), kv_buf1, &vq[1]));
         page_q = load_page(2);
@@ -688,7 +693,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const fa_mla_de
       }
     };
     prologue(true);
-    if constexpr (kMode == kDense) load_q();
     fp8_first_tile();
 
     float mref_start[2] = {ninf, ninf};
