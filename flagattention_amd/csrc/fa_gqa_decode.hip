@@ -456,11 +456,14 @@ __global__ __launch_bounds__(kGThreads, D <= 128 ? 2 : 1) void gqa_decode_kernel
 // that runs ahead never overwrites a slot still being read), in the same order in every
 // wave, so every wave holds the same S^T and runs the same online softmax; then O^T +=
 // V^T P^T over its dims.  The wave's 8 KB K and V slices of a tile are both copied
-// HBM -> LDS (double-buffered per wave), requested together at the start of the step
-// before their tile's, so each has a whole step to land.  (With K loaded into VGPRs
+// HBM -> LDS, double-buffered per wave; the slices are the wave's own, so a buffer is
+// free as soon as the wave itself has read it.  K of tile u+2 is requested right after
+// QK(u) has read tile u's K, V of tile u+1 at the start of step u (PV(u-1) has read its
+// buffer): 24 KB per wave in flight during PV, 16 KB during QK.  (K requested with V at
+// the start of the step before its tile's, 16 KB in flight: 404 us at the benchmark
+// shape, B = 64, 32 heads, context 4,096, against 358 us.  With K loaded into VGPRs
 // instead, the compiler's wait for K counts only K loads and would also drain V copies
-// issued after them, which kept V requested only half a step ahead: 426 us at the
-// benchmark shape, B = 64, 32 heads, context 4,096.)
+// issued after them, which kept V requested only half a step ahead: 426 us.)
 constexpr int kWideD = 512;
 constexpr int kWideDims = kWideD / 4;  // dims per wave
 
@@ -558,12 +561,13 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
                                                   mm * a.q_stride_m + dim0 + 32 * kk + 8 * G)
                     : T8{};
 
-  // Step u requests K and V of tile u+1 at its start and waits for those of
-  // tile u (16 copies per wave and tile, counted in vmcnt; the loop issues no
-  // other vector memory operation).  K slice layout: copy c = (token half h,
-  // k-step kk) = 4h + kk holds, at 16 l, lane l's operand: token 16h + l % 16,
-  // dims dim0 + 32kk + 8 (l / 16)..+7, so the QK reads are 16 consecutive bytes
-  // per lane.
+  // Step u requests V of tile u+1 at its start, waits for K and V of tile u (8 + 8
+  // copies per wave and tile, counted in vmcnt; the loop issues no other vector
+  // memory operation), and requests K of tile u+2 after its QK; the issue order
+  // is K(u), V(u), K(u+1), V(u+1) at every wait.  K slice layout: copy c = (token
+  // half h, k-step kk) = 4h + kk holds, at 16 l, lane l's operand: token 16h + l % 16,
+  // dims dim0 + 32kk + 8 (l / 16)..+7, so the QK reads are 16 consecutive bytes per
+  // lane.
   unsigned int kmask[2] = {0u, 0u};
   auto issue_v = [&](int u, auto bt, auto tt) {
     constexpr int buf = decltype(bt)::value;
@@ -616,15 +620,13 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
     constexpr int buf = decltype(bt)::value;
     __builtin_amdgcn_sched_barrier(0);
     if (has_next) {
-      // K(u+1) and V(u+1) into the other buffers, last read by QK(u-1) / PV(u-1)
-      // of this wave
-      issue_k(u + 1, IntTag<buf ^ 1>{}, tt);
+      // V(u+1) into the other V buffer, last read by PV(u-1) of this wave
       issue_v(u + 1, IntTag<buf ^ 1>{}, tt);
       __builtin_amdgcn_sched_barrier(0);
       // in flight, oldest first: K(u), V(u), K(u+1), V(u+1): K(u) and V(u) landed
       wait_vmem<kKLoads + kCopies>();
     } else {
-      wait_vmem<0>();
+      wait_vmem<0>();  // K(u+1) was not requested either
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -641,6 +643,13 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
         s[h] = mfma_16x16x32(kv, qf[kk], s[h]);
       }
       sx[u & 1][wave][h][lane] = s[h];
+    }
+    // K(u+2) into the K buffer QK(u) has just read (this wave's slice only)
+    const unsigned int km_u = kmask[buf];
+    if (u + 2 < ntiles) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_k(u + 2, IntTag<buf>{}, tt);
+      __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("" ::: "memory");
     barrier();
@@ -664,7 +673,7 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = 16 * h + 4 * G + i;
-        const bool ok = tile_start + j < lim && ((kmask[buf] >> j) & 1u);
+        const bool ok = tile_start + j < lim && ((km_u >> j) & 1u);
         sv[h][i] = ok ? s[h][i] * scale_log2 : ninf;
         tmax = fmaxf(tmax, sv[h][i]);
       }
@@ -705,6 +714,7 @@ __global__ __launch_bounds__(kGThreads, 1) void gqa_decode_wide_kernel(
   auto run = [&](auto tt) {
     issue_k(0, IntTag<0>{}, tt);
     issue_v(0, IntTag<0>{}, tt);
+    if (ntiles > 1) issue_k(1, IntTag<1>{}, tt);
     int u = 0;
     for (;;) {
       const bool n1 = u + 1 < ntiles;
