@@ -313,6 +313,22 @@ def test_flash_attention_head_size_512(M, N, causal):
         assert float((lse.cpu() - lse_ref).abs().max()) <= 1e-3
 
 
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 65, 96, 97, 128])
+def test_flash_attention_head_size_512_few_tiles(N):
+    """One to four 32-token tiles per work-group at head dim 512: the dims-split loop
+    requests K two tiles ahead and V one, so these are its pipeline's start and end cases
+    (no next tile, a next tile without the one after it)."""
+    need_gpu()
+    q, k, v = _splitkv_inputs(3, 8, 2, 1, N, 512, torch.float16, "BHTD", 1.0, 700 + N)
+    o_ref, lse_ref = _oracle_chunked(q, k, v, False, True)
+    o_low, _ = _oracle_chunked(q, k, v, False, False)
+    o, lse, _, _, _ = flag_attn.flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), False,
+                                                return_log_normalizer=True)
+    torch.cuda.synchronize()
+    assert_lowp_rule(o.cpu(), o_ref, o_low)
+    assert float((lse.cpu() - lse_ref).abs().max()) <= 1e-3
+
+
 @pytest.mark.parametrize("head_size", [64, 512])
 def test_paged_attention_split_longer_than_lds_table(head_size):
     """A split of more than 2,048 pages (8-token pages, one split over 20,000 tokens): the
