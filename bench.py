@@ -18,8 +18,9 @@ slower.
 
 With no --workload (the default invocation) the line also carries `other_workloads`: every
 other workload above, measured briefly in the same process after the flagship (OTHER_STEPS
-timed steps each, no CPU baseline) -- its µs/step, its kernel's mean time by events and
-roofline fraction -- so that one default run records every workload; --no-extras skips it.
+timed steps each, no CPU baseline, an OTHER_SETTLE_S settle phase) -- its µs/step, its
+kernel's mean time by events and roofline fraction -- so that one default run records every
+workload; --no-extras skips it.
 
 Prints one JSON line: value = wall-clock us/step (lower is better); `roofline` is the
 decode kernel alone (HIP events around its launch on the launch stream, on every k-th
@@ -51,6 +52,10 @@ PAGE = 64
 EVENT_EVERY = 8  # at most this many timed steps per decode launch bracketed by events
 MIN_EVENT_LAUNCHES = 10  # ...and at least this many bracketed launches
 SETTLE_S = 0.25  # seconds of untimed steps (warm-up included) before the timed region
+# ... for the other workloads of the default run: right after the compute-bound MLA steps a
+# memory-bound one needs ~0.5 s of its own steps to reach its sustained rate (paged GQA
+# measured 5% slow with 0.25 s, at its standalone rate with 0.5 s)
+OTHER_SETTLE_S = 1.0
 COPY_BYTES = 512 << 20  # calibration copy of --traffic-calibrate
 # the default run (no --workload) also measures these, briefly, into `other_workloads`
 OTHER_WORKLOADS = ("skew", "sparse", "sparse_fp8", "gqa_paged", "gqa_splitkv", "gqa_paged_d512",
@@ -204,6 +209,11 @@ def with_traffic_source(rec: dict) -> dict:
     if rec["roofline"].get("traffic") is not None:
         rec["roofline"]["traffic_source"] = TRAFFIC_SOURCE
     return rec
+
+
+def settle_seconds(args) -> float:
+    """The settle phase's length: SETTLE_S, or the run's own (other workloads)."""
+    return getattr(args, "settle_s", SETTLE_S)
 
 
 def calibrate_then(step, args, name: str) -> None:
@@ -360,7 +370,7 @@ def run_gqa(args) -> dict:
         step(i)
     torch.cuda.synchronize()
     settle_steps = 0
-    while time.perf_counter() - t_warm < SETTLE_S:
+    while time.perf_counter() - t_warm < settle_seconds(args):
         for _ in range(20):
             step(settle_steps)
             settle_steps += 1
@@ -468,7 +478,7 @@ def run_topk(args) -> dict:
         step(i)
     torch.cuda.synchronize()
     settle_steps = 0
-    while time.perf_counter() - t_warm < SETTLE_S:
+    while time.perf_counter() - t_warm < settle_seconds(args):
         for _ in range(20):
             step(settle_steps)
             settle_steps += 1
@@ -564,7 +574,7 @@ def run_kvcache(args) -> dict:
         step(i)
     torch.cuda.synchronize()
     settle_steps = 0
-    while time.perf_counter() - t_warm < SETTLE_S:
+    while time.perf_counter() - t_warm < settle_seconds(args):
         for _ in range(20):
             step(settle_steps)
             settle_steps += 1
@@ -679,6 +689,7 @@ def other_workloads(args) -> dict:
     for w in OTHER_WORKLOADS:
         sub = argparse.Namespace(**vars(args))
         sub.workload, sub.steps, sub.warmup, sub.no_cpu_baseline = w, OTHER_STEPS, OTHER_WARMUP, True
+        sub.settle_s = OTHER_SETTLE_S
         try:
             r = run_workload(sub)
             ro = r["roofline"]
@@ -721,7 +732,7 @@ def run_mla(args) -> dict | None:
         step(i)
     torch.cuda.synchronize()
     settle_steps = 0
-    while time.perf_counter() - t_warm < SETTLE_S:
+    while time.perf_counter() - t_warm < settle_seconds(args):
         for _ in range(20):
             step(settle_steps)
             settle_steps += 1
